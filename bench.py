@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""GRINQH quantized-linear benchmark on one MI355X.
+
+Workload (the decode sweep): Llama-3-8B linear shapes
+qkv 4096->6144, o_proj 4096->4096, gate_up 4096->28672, down 14336->4096 at
+M in {1, 4, 16, 64}; fp16 activations N(0,1) with 1 % of channels x20; weights
+0.02*N(0,1) RTN-quantised to int8 codes per 128-row group with fp16 scales;
+union grading with thresholds [0, P50, P80, P95] of sigma_k = max_m |x[m,k]|.
+One step = the 16 products once.  Weights rotate through enough copies to
+exceed 2x the 256 MB MALL, so timings reflect HBM.
+
+value = whole-step HBM throughput in algorithmic bytes (planes actually needed
+by the grading + scales + x + y) per second.  The JSON line also carries the
+per-case kernel times, the roofline of the dominant kernel, the prefill
+TFLOP/s at M=2048 (BASELINE configs[2] shapes, dense) and the CPU baseline
+(the reference's pure-PyTorch math on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "vllm-grinqh-plugin_amd"))
+sys.path.insert(0, REPO)
+
+METRIC = "GEMM TFLOP/s + HBM GB/s (% roofline) at Llama-3-8B shapes, M=1/16/2048"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+SHAPES = [("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
+DECODE_M = [1, 4, 16, 64]
+PREFILL_M = 2048
+GS = 128
+BITS = 8
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synth_weight(torch, K: int, N: int, seed: int, device):
+    """0.02*N(0,1) weights, symmetric RTN per 128-row group to int8 codes with
+    fp16 scales, in the loader's [K, N] / [K/128, N] layout."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    wf = 0.02 * torch.randn((N, K), generator=g, device=device, dtype=torch.float32)
+    wg = wf.view(N, K // GS, GS)
+    lim = (1 << (BITS - 1)) - 1
+    s = (wg.abs().amax(-1) / lim).clamp_min(1e-8).half()
+    q = torch.clamp(torch.round(wg / s.float().unsqueeze(-1)), -lim - 1, lim).to(torch.int8)
+    return q.view(N, K).t().contiguous(), s.t().contiguous()
+
+
+def synth_x(torch, M: int, K: int, seed: int, device):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((M, K), generator=g)
+    out = torch.randperm(K, generator=g)[: math.ceil(K / 100)]
+    x[:, out] *= 20
+    return x.half().to(device)
+
+
+def thresholds_for(x, q=(0.5, 0.8, 0.95)):
+    sigma = x.abs().float().amax(0).cpu().numpy()
+    return [0.0] + [float(v) for v in np.quantile(sigma, q)]
+
+
+def decode_bytes(bits_per_row, K, N, M):
+    planes = int(bits_per_row.sum()) * (N // 4)
+    return planes + (K // GS) * N * 2 + M * K * 2 + M * N * 2
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=20, help="launches per case graph for kernel timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the GRINQH hot path has no sharded path "
+                                   "(one process, one MI355X); run with --gpus 1"}))
+        return 2
+
+    import torch
+    from grinqh import _lib
+    from grinqh.kernel import run_product
+    from grinqh.utils import grade, prepare_weight
+
+    _lib.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"device {torch.cuda.get_device_name(dev)}")
+
+    # ---------------- weights (rotated copies to defeat the MALL)
+    base = {}
+    plane_bytes = 0
+    for i, (name, K, N) in enumerate(SHAPES):
+        w, s = synth_weight(torch, K, N, 1000 + i, dev)
+        base[name] = (prepare_weight(w, BITS), s)
+        plane_bytes += base[name][0].numel() * 4 + s.numel() * 2
+        del w
+    n_copies = max(2, math.ceil(3 * MALL_BYTES / plane_bytes))
+    copies = {name: [base[name]] + [(p.clone(), s.clone()) for _ in range(n_copies - 1)]
+              for name, (p, s) in base.items()}
+    log(f"weights ready: {plane_bytes / 1e6:.1f} MB per copy x {n_copies} copies")
+
+    # ---------------- cases
+    cases = []
+    for i, (name, K, N) in enumerate(SHAPES):
+        for M in DECODE_M:
+            x = synth_x(torch, M, K, 17 * i + M, dev)
+            t = thresholds_for(x)
+            zb, _ = grade(x, t, BITS)
+            bits = np.unpackbits(zb.cpu().numpy()[:, None], axis=1).sum(1)
+            cases.append(dict(shape=name, K=K, N=N, M=M, x=x, t=t, bytes=decode_bytes(bits, K, N, M),
+                              mean_planes=float(bits.mean())))
+
+    def call(c, r):
+        p, s = copies[c["shape"]][r]
+        return run_product(c["x"], p, s, None, BITS, GS, c["N"] // 4, c["t"], "union")
+
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for c in cases:  # size the per-stream workspace before any capture
+            call(c, 0)
+    torch.cuda.synchronize()
+
+    # per-case kernel time: graph of `reps` launches cycling the weight copies
+    for c in cases:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                for j in range(args.reps):
+                    call(c, j % n_copies)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(3):
+                g.replay()
+            e1.record(stream)
+        e1.synchronize()
+        c["us"] = e0.elapsed_time(e1) * 1e3 / (3 * args.reps)
+        c["gbs"] = c["bytes"] / (c["us"] * 1e-6) / 1e9
+        log(f"{c['shape']:8s} M={c['M']:3d} planes/row={c['mean_planes']:.2f} {c['bytes'] / 1e6:7.2f} MB "
+            f"{c['us']:8.2f} us {c['gbs']:8.1f} GB/s ({100 * c['gbs'] / HBM_PEAK_GBS:.1f}% HBM)")
+        del g
+
+    # ---------------- the step: one graph per weight copy holding all 16 products
+    step_graphs = []
+    for r in range(n_copies):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                for c in cases:
+                    call(c, r)
+        step_graphs.append(g)
+    for i in range(args.warmup):
+        step_graphs[i % n_copies].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for i in range(args.steps):
+            step_graphs[i % n_copies].replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    step_bytes = sum(c["bytes"] for c in cases)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"step {ms_per_step * 1e3:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s)")
+
+    # dominant kernel: the M<=16 decode kernel instantiation (12 of 16 launches per step)
+    dom = [c for c in cases if c["M"] <= 16]
+    dom_bytes = sum(c["bytes"] for c in dom) / len(dom)
+    dom_us = sum(c["us"] for c in dom) / len(dom)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "grinqh::decode_kernel<F16,1,4,false>", "bytes_per_launch": int(dom_bytes),
+                "avg_launch_us": round(dom_us, 3)}
+
+    # ---------------- prefill at M=2048 (dense dequantize-then-matmul, reference dispatch for M>1)
+    prefill = None
+    if not args.no_prefill:
+        prefill = []
+        for i, (name, K, N) in enumerate(SHAPES):
+            x = synth_x(torch, PREFILL_M, K, 99 + i, dev)
+            p, s = copies[name][0]
+            with torch.cuda.stream(stream):
+                run_product(x, p, s, None, BITS, GS, N // 4, [0.0] * 4, "dense")
+                torch.cuda.synchronize()
+                e0.record(stream)
+                n_it = 5
+                for j in range(n_it):
+                    pj, sj = copies[name][j % n_copies]
+                    run_product(x, pj, sj, None, BITS, GS, N // 4, [0.0] * 4, "dense")
+                e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / n_it
+            tf = 2.0 * PREFILL_M * K * N / (us * 1e-6) / 1e12
+            prefill.append({"shape": name, "M": PREFILL_M, "us": round(us, 2), "tflops": round(tf, 1),
+                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+            log(f"prefill {name:8s} M={PREFILL_M} {us:9.1f} us {tf:7.1f} TFLOP/s")
+
+    # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import cpu_reference
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        sample = [c for c in cases if c["M"] == 1]
+        tot_b, tot_t = 0, 0.0
+        for c in sample:
+            p, s = copies[c["shape"]][0]
+            pc, sc, xc = p.cpu(), s.cpu(), c["x"].cpu()
+            cpu_reference.graded(xc, pc, sc, c["t"], GS, BITS)  # warmup
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                cpu_reference.graded(xc, pc, sc, c["t"], GS, BITS)
+                ts.append(time.perf_counter() - t0)
+            tot_t += float(np.median(ts))
+            tot_b += c["bytes"]
+        cpu = {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": "graded union math of the reference (masked fp32 weights + matmul, torch CPU eager) on the "
+                         "four decode shapes at M=1, median of 3 after 1 warmup",
+               "cpu": _cpu_model()}
+        log(f"cpu baseline {cpu['value']} GB/s on {cores} cores")
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "decode sweep (BASELINE configs[1]): Llama-3-8B qkv/o_proj/gate_up/down x "
+                               "M=1,4,16,64, union grading t=[0,P50,P80,P95], max_bits 8, group 128",
+                   "weight_copies": n_copies, "frac_of_hbm_roofline": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "cases": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in c.items() if k not in ("x", "t")}
+                  for c in cases],
+        "prefill": prefill,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,122 @@
+/*
+ * grinqh.h -- C ABI of libgrinqh_hip.so, the MI355X (gfx950) implementation of
+ * the GRINQH quantized-linear hot path.
+ *
+ * Plain C: device pointers, sizes, an int status and a HIP stream passed as
+ * `void*` (a hipStream_t; NULL = the default stream).  No torch or HIP types
+ * appear in the signatures.  Every call only enqueues work on `stream`; none
+ * synchronises the host, so all of them may be captured in a HIP graph.
+ *
+ * Reference paths below are relative to the otcathatsya/vllm-grinqh-plugin
+ * checkout.
+ *
+ * Packed weight layout ("planes"): uint32 [K][Z][N/16], Z = max_bits/2, the
+ * same bytes the reference's process_weights_after_loading produces
+ * (grinqh/grinqh.py:200-210 -> grinqh/utils.py:17-22 and 100-146).  Word
+ * (k, z, c) holds, in byte beta / slot j (bits 8*beta+7-2j .. 8*beta+6-2j), the
+ * 2-bit digit z (most significant first) of W[k][(4j+beta)*(N/16) + c].
+ */
+#ifndef GRINQH_H_
+#define GRINQH_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (0 = success) */
+#define GRINQH_OK 0
+#define GRINQH_ERR_INVALID 1     /* bad shape / dtype / bit width / alignment: ValueError in Python */
+#define GRINQH_ERR_HIP 2         /* HIP launch error: RuntimeError in Python */
+#define GRINQH_ERR_WORKSPACE 3   /* workspace missing or smaller than grinqh_workspace_bytes() */
+
+/* activation / scale / output dtype */
+#define GRINQH_DTYPE_F16 0
+#define GRINQH_DTYPE_BF16 1
+
+/* batch grading mode for grinqh_gemm_or_gemv */
+#define GRINQH_MODE_REFERENCE 0  /* rows == 1: graded GEMV, rows > 1: dense (grinqh/kernel.py:663-680) */
+#define GRINQH_MODE_UNION 1      /* every batch graded on sigma_k = max_m |x[m][k]| (grinqh/kernel.py:170-360) */
+#define GRINQH_MODE_DENSE 2      /* never graded: all planes, no midpoint bias */
+
+/* Version of this ABI (bumped on any signature or semantic change). */
+int grinqh_abi_version(void);
+
+/* Static description of a status code. */
+const char* grinqh_status_string(int status);
+
+/* Plane pack of already preshuffled + shifted codes.
+ * Replaces pack_triton / _pack_kernel_uint32 (grinqh/utils.py:100-146).
+ * codes_u8: uint8 [K][N] (16-byte aligned rows), planes_u32: uint32 [K][max_bits/2 * N/16].
+ * N % 16 == 0, max_bits in {2,4,6,8}. */
+int grinqh_pack_planes(const void* codes_u8, void* planes_u32, int64_t K, int64_t N, int max_bits,
+                       void* stream);
+
+/* Load-time preparation of a logical int8 weight W[K][N] (input-major, as the
+ * weight loader leaves it): preshuffle, shift by 8-max_bits, plane pack.
+ * Replaces the data path of GRINQHLinearMethod.process_weights_after_loading
+ * (grinqh/grinqh.py:200-210: grinqh_input_preshuffle, <<, pack_triton). */
+int grinqh_prepare_weight(const void* w_int8, void* planes_u32, int64_t K, int64_t N, int max_bits,
+                          void* stream);
+
+/* Unpack the unsigned b-bit codes of selected rows, in preshuffled column order:
+ * codes_u32 is uint32 [n_rows][N/4] whose bytes are U >> (8-b).
+ * Replaces unpack_pyt / unpack_triton (grinqh/utils.py:149-177, 180-223).
+ * rows: int64 device array of n_rows row indices, each in [0, K) (not checked on the device).
+ * bit_level = Z in 1..4. */
+int grinqh_unpack_planes(const void* planes_u32, const int64_t* rows, int64_t n_rows, void* codes_u32,
+                         int64_t K, int64_t N, int bit_level, void* stream);
+
+/* Dense dequantisation in logical column order: out[k][n] = RNE(W[k][n] * scale[k/gs][n])
+ * in `dtype`, or the int8 W itself when scale == NULL (out is then int8 [K][N]).
+ * Replaces the unpack / sign-extend / postshuffle / scale steps of
+ * grinqh_prefill_gemm_compiled (grinqh/kernel.py:568-586). */
+int grinqh_dequantize(const void* planes_u32, const void* scale, void* out, int64_t K, int64_t N,
+                      int max_bits, int group_size, int dtype, void* stream);
+
+/* Grading export: zone bits (bit z = zone z active) and midpoint bias of every
+ * weight row k for sigma_k = max_{m<M} |x[m][k]| (M == 1: |x[k]|), compared as
+ * fp32(sigma) > thresholds[z] (strict; thresholds already rounded to fp32).
+ * Replaces the inline grading of grinqh/kernel.py:98-114 (one row) and
+ * :249-289 (batch union).  beta may be NULL. */
+int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, int max_bits,
+                 const float thresholds[4], uint8_t* zone_bits, int32_t* beta, void* stream);
+
+/* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none).  The
+ * first 4096 bytes are counters: zero them once when the workspace is
+ * allocated; every call leaves them zero again.  Calls that share a workspace
+ * must be ordered (same stream). */
+size_t grinqh_workspace_bytes(int64_t M, int64_t K, int64_t N, int max_bits, int mode);
+
+/* The quantized linear y[M][N] = x[M][K] * W_eff (+ bias), x/scale/bias/y in `dtype`.
+ * Replaces torch.ops.grinqh.gemm_or_gemv (grinqh/kernel.py:646-710); N here is
+ * 4 * original_n.  thresholds: 4 fp32 values (zero padded like
+ * grinqh/grinqh.py:111).  x rows are ldx elements apart (ldx % 8 == 0), y is
+ * dense [M][N].  K % 32 == 0, N % 16 == 0, group_size % 32 == 0. */
+int grinqh_gemm_or_gemv(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                        const void* planes_u32, const void* scale, const void* bias, void* y,
+                        int max_bits, int group_size, const float thresholds[4], int mode,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Batch-union GEMV: grinqh_gemm_or_gemv with GRINQH_MODE_UNION.
+ * Replaces grinqh_gemv_batch_union (grinqh/kernel.py:607-643). */
+int grinqh_gemv_batch_union(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                            const void* planes_u32, const void* scale, const void* bias, void* y,
+                            int max_bits, int group_size, const float thresholds[4],
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Dense dequantize-then-matmul for any M: grinqh_gemm_or_gemv with GRINQH_MODE_DENSE.
+ * Replaces grinqh_prefill_gemm_compiled (grinqh/kernel.py:561-587) and, for
+ * max_bits == 4, the Marlin path (grinqh/kernel.py:528-558). */
+int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                         const void* planes_u32, const void* scale, const void* bias, void* y,
+                         int max_bits, int group_size, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRINQH_H_ */

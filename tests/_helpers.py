@@ -1,0 +1,70 @@
+"""Shared test helpers: seeded inputs in the reference tests' style and the
+output tolerance used by every floating-point parity check."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# Unit roundoff of the output dtypes.
+UNIT_ROUNDOFF = {"float16": 2.0 ** -11, "bfloat16": 2.0 ** -8}
+TORCH_DTYPES = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def rand_weight(rng: np.random.Generator, K: int, N: int, b: int) -> np.ndarray:
+    """Uniform b-bit signed codes (reference tests: torch.randint(-limit-1, limit+1))."""
+    lim = (1 << (b - 1)) - 1
+    return rng.integers(-lim - 1, lim + 1, size=(K, N), dtype=np.int64).astype(np.int8)
+
+
+def to_dtype_np(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float64/float32 values into fp16/bf16 and back to float64 (RNE)."""
+    return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(TORCH_DTYPES[dtype]).double().numpy()
+
+
+def dense_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, dtype: str, group_size: int = 128):
+    """Largest difference the reference's own elementwise rounding of W*s to
+    the activation dtype (grinqh/kernel.py:586) can make to a dense product:
+    u * (|x| @ |W*s|).  Kernels that keep W*s exact (scale applied in fp32)
+    may differ from the reference's dense output by up to this much."""
+    u = UNIT_ROUNDOFF[dtype]
+    s = np.repeat(np.abs(np.asarray(scale, dtype=np.float64)), group_size, axis=0)[: W.shape[0]]
+    return u * (np.abs(np.asarray(x, dtype=np.float64)) @ (np.abs(W.astype(np.float64)) * s))
+
+
+def output_tolerance(ref_pre: np.ndarray, dtype: str, bias=None) -> np.ndarray:
+    """Allowed |y - y_ref| for a kernel output against the float64 oracle.
+
+    ``ref_pre`` is the oracle's float64 product before the output cast.  The
+    kernel output carries two roundings in the output dtype (cast, then bias
+    add, as in grinqh/kernel.py:706-708) -- up to 2 units of roundoff of the
+    result each -- plus fp32 accumulation-order differences, bounded here by
+    2e-3 of the product's rms (the tolerance stated for this path).
+    """
+    u = UNIT_ROUNDOFF[dtype]
+    ref = np.asarray(ref_pre, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(ref[np.isfinite(ref)] ** 2))) if np.isfinite(ref).any() else 0.0
+    mag = np.abs(ref)
+    if bias is not None:
+        mag = mag + np.abs(ref + np.asarray(bias, dtype=np.float64)[None, :])
+    return 2.0 * u * mag + 2e-3 * rms + 1e-30
+
+
+def assert_output_close(y: torch.Tensor, ref_pre: np.ndarray, ref_final: np.ndarray, dtype: str, bias=None,
+                        what: str = "", extra_tol=None) -> dict:
+    """Check a kernel output against the oracle and report max abs / rel error."""
+    got = y.detach().float().cpu().double().numpy().reshape(ref_final.shape)
+    tol = output_tolerance(ref_pre.reshape(ref_final.shape), dtype, bias)
+    if extra_tol is not None:
+        tol = tol + np.asarray(extra_tol).reshape(ref_final.shape)
+    err = np.abs(got - ref_final)
+    nan_ref = np.isnan(ref_final)
+    assert np.array_equal(np.isnan(got), nan_ref), f"{what}: NaN pattern differs"
+    ok = ~nan_ref
+    bad = err[ok] > tol[ok]
+    rel = err[ok] / np.maximum(np.abs(ref_final[ok]), 1e-30)
+    stats = {"max_abs": float(err[ok].max()) if ok.any() else 0.0,
+             "max_rel": float(rel.max()) if ok.any() else 0.0}
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {bad.size} outputs outside tolerance; "
+                           f"max abs err {stats['max_abs']:.3e}, worst excess "
+                           f"{float((err[ok] - tol[ok]).max()):.3e}")
+    return stats

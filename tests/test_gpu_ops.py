@@ -1,0 +1,336 @@
+"""GPU parity tests of the gfx950 GRINQH kernels against the CPU oracle.
+
+Mirrors the reference's tests/test_grinqh_ops.py case by case (names and
+parametrisation), with the reference's dense restatements replaced by the
+float64 oracle (oracle/grinqh_oracle.py) on the same seeded inputs, and adds
+bit-exact checks of the integer path (pack, unpack, dequantisation, grading).
+Every call goes through libgrinqh_hip.so.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import grinqh_oracle as O
+from tests._helpers import TORCH_DTYPES, assert_output_close, dense_rounding_bound, rand_weight, to_dtype_np
+
+pytestmark = pytest.mark.gpu
+
+BITS = [2, 4, 6, 8]
+DTYPES = ["float16", "bfloat16"]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from grinqh import _lib
+    _lib.load_library()
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _setup(rng, K, N, b, dtype, M=1, scale_sd=1.0):
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)), dtype)
+    s = to_dtype_np(rng.standard_normal((math.ceil(K / 128), N)) * scale_sd, dtype)
+    return W, x, s
+
+
+def _prepare(W, b):
+    from grinqh.utils import prepare_weight
+    return prepare_weight(_dev(W), b)
+
+
+def _tdt(x, dtype):
+    return torch.from_numpy(x.astype(np.float32)).to(TORCH_DTYPES[dtype]).cuda()
+
+
+# ----------------------------------------------------------------------- integer path
+
+@pytest.mark.parametrize("bit_level", [1, 2, 3, 4])
+@pytest.mark.parametrize("backend", ["rows", "vectorised"])
+def test_pack_unpack(bit_level, backend):
+    """Reference tests/test_grinqh_ops.py:58-88 plus bitwise equality with the
+    oracle's plane pack."""
+    from grinqh.utils import BitLevel, pack_planes, unpack_planes
+    rng = np.random.default_rng(bit_level)
+    b = 2 * bit_level
+    A = rng.integers(0, 256, size=(384, 320), dtype=np.int64).astype(np.uint8)
+    B = pack_planes(_dev(A).view(torch.uint32), max_bits=b)
+    assert B.numel() * B.element_size() == A.size * b // 8
+    np.testing.assert_array_equal(B.cpu().numpy(), O.pack_planes(A, b))
+    lvl = BitLevel(bit_level)
+    if backend == "rows":
+        rec = np.stack([unpack_planes(B, i, lvl, 320 // 4).view(torch.uint8).cpu().numpy()[0] for i in range(384)])
+    else:
+        rec = unpack_planes(B, torch.arange(384), lvl, 320 // 4).view(torch.uint8).cpu().numpy()
+    np.testing.assert_array_equal(rec, A >> (8 - b))
+
+
+@pytest.mark.parametrize("b", BITS)
+@pytest.mark.parametrize("shape", [(256, 256), (384, 320), (128, 4096), (64, 28672)])
+def test_prepare_weight_bit_exact(b, shape):
+    rng = np.random.default_rng(b * 7 + shape[1])
+    W = rand_weight(rng, *shape, b)
+    np.testing.assert_array_equal(_prepare(W, b).cpu().numpy(), O.prepare_weight(W, b))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("b", BITS)
+def test_dequantize_bit_exact(b, dtype):
+    """Integer unpack and the S9 element W*s (grinqh/kernel.py:568-586), bitwise."""
+    from grinqh.utils import dequantize
+    rng = np.random.default_rng(30 + b)
+    W, _, s = _setup(rng, 384, 320, b, dtype)
+    P = _prepare(W, b)
+    np.testing.assert_array_equal(dequantize(P, None, b, 128, 80).cpu().numpy(), W)
+    got = dequantize(P, _tdt(s, dtype), b, 128, 80).double().cpu().numpy()
+    np.testing.assert_array_equal(got, O.dense_weight(W, s, 128, dtype))
+
+
+def _grade_cases(dtype):
+    f = np.float16 if dtype == "float16" else np.float32
+    one = 1.0
+    nxt = float(np.nextafter(np.float16(one), np.float16(2))) if dtype == "float16" else 1.0078125
+    vals = np.array([0.0, -0.0, one, -one, nxt, 0.5, np.inf, -np.inf, np.nan, 1e-4, 3.0, -7.5, 65504.0],
+                    dtype=np.float64)
+    return vals, [
+        [one, 0.5, 2.0, 3.0],                       # ties at |x| == t
+        [0.5 * (one + nxt), 0.0, -1.0, 1e30],       # threshold between adjacent representable values
+        [1.0 - 1e-12, 2.5, 0.25, 0.0],              # non-monotone; rounds to 1.0 in fp32
+        [-1.0] * 4,
+        [float("inf")] * 4,
+        [0.1, 0.2],                                 # short list: zero padded
+    ]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("b", BITS)
+def test_grade_bit_exact(b, dtype):
+    from grinqh.utils import grade
+    vals, tsets = _grade_cases(dtype)
+    rng = np.random.default_rng(40 + b)
+    for t in tsets:
+        for M in (1, 3):
+            x = np.tile(vals, (M, 1)) if M == 1 else np.concatenate(
+                [vals[None, :], to_dtype_np(rng.standard_normal((M - 1, vals.size)), dtype)])
+            xt = _tdt(x, dtype)
+            bits, beta = grade(xt, t, b)
+            xs = xt.double().cpu().numpy()
+            sigma = np.fmax.reduce(np.abs(xs), axis=0)
+            eb = O.grade(sigma, t, b)
+            np.testing.assert_array_equal(bits.cpu().numpy(), eb, err_msg=f"t={t} M={M}")
+            np.testing.assert_array_equal(beta.cpu().numpy(), O.midpoint_bias(eb, b))
+
+
+# ----------------------------------------------------------------------- products
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+def test_dense_prefill_matches_reference(max_bits, dtype):
+    """Reference tests/test_grinqh_ops.py:91-124 (X[16,384] @ (W*s), W[384,320])."""
+    from grinqh.kernel import grinqh_prefill_dense
+    rng = np.random.default_rng(50 + max_bits)
+    W, x, s = _setup(rng, 384, 320, max_bits, dtype, M=16)
+    y = grinqh_prefill_dense(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), 128, 80, max_bits)
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="dense prefill",
+                        extra_tol=dense_rounding_bound(x, W, s, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+def test_dense_gemv_matches_reference(max_bits, dtype):
+    """Reference tests/test_grinqh_ops.py:156-190: thresholds -1 -> all planes."""
+    rng = np.random.default_rng(60 + max_bits)
+    W, x, s = _setup(rng, 256, 256, max_bits, dtype)
+    t = [-1.0] * 4
+    y = torch.ops.grinqh.gemm_or_gemv(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128,
+                                      64, t)
+    pre = O.gemv_f64(x, W, s, t, max_bits, 128)
+    ref = x.astype(np.float64) @ (W.astype(np.float64) * np.repeat(s, 128, 0))
+    np.testing.assert_allclose(pre, ref, rtol=1e-12, atol=1e-9)
+    assert_output_close(y, pre, O.gemv(x, W, s, None, t, max_bits, 128, dtype), dtype, what="dense gemv")
+
+
+QUANTILES = {
+    "spread": [0.2, 0.4, 0.6, 0.8],
+    "all_or_nothing": [0.5] * 4,
+    "mild": [0.1, 0.2, 0.3, 0.4],
+    "aggressive": [0.6, 0.7, 0.8, 0.9],
+    "skip_all": [1.0] * 4,
+}
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+@pytest.mark.parametrize("quantiles", list(QUANTILES.values()), ids=list(QUANTILES.keys()))
+def test_gemv_thresholds_match_reference(max_bits, dtype, quantiles):
+    """Reference tests/test_grinqh_ops.py:193-240: thresholds at quantiles of |x|."""
+    rng = np.random.default_rng(70 + max_bits)
+    W, x, s = _setup(rng, 256, 256, max_bits, dtype)
+    nz = max_bits // 2
+    t = np.quantile(np.abs(x).astype(np.float32).reshape(-1), quantiles).tolist()[:nz]
+    t = t + [0.0] * (4 - nz)
+    y = torch.ops.grinqh.gemm_or_gemv(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128,
+                                      64, t)
+    pre = O.gemv_f64(x, W, s, t, max_bits, 128)
+    stats = assert_output_close(y, pre, O.gemv(x, W, s, None, t, max_bits, 128, dtype), dtype, what="graded gemv")
+    if quantiles == QUANTILES["skip_all"]:
+        assert torch.count_nonzero(y).item() == 0
+    assert stats["max_abs"] >= 0.0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+@pytest.mark.parametrize("batch_size", [2, 3, 5, 8])
+def test_batch_union_gemv_matches_looped_gemv(batch_size, max_bits, dtype):
+    """Reference tests/test_grinqh_ops.py:245-282 (all-active thresholds): the
+    union GEMV equals the per-row GEMV loop and the masked dense reference."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(80 + batch_size)
+    W, x, s = _setup(rng, 256, 256, max_bits, dtype, M=batch_size)
+    t = [-1.0] * 4
+    P = _prepare(W, max_bits)
+    xt, st = _tdt(x, dtype), _tdt(s, dtype)
+    yb = grinqh_gemv_batch_union(xt, P, st, None, max_bits, 128, 64, t)
+    yl = torch.cat([torch.ops.grinqh.gemm_or_gemv(xt[i:i + 1], P, st, None, max_bits, 128, 64, t)
+                    for i in range(batch_size)])
+    pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
+    fin = O.gemv_union(x, W, s, None, t, max_bits, 128, dtype)
+    assert_output_close(yb, pre, fin, dtype, what="union")
+    assert_output_close(yl, pre, fin, dtype, what="looped")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 4, 16, 17, 33, 64, 65, 130])
+def test_union_graded_batches(M, max_bits, dtype):
+    """Union grading at thresholds that make every zone occur (P50/P80/P95 of
+    sigma), across the 1/2/4 m-tile kernels and the multi-launch path."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(90 + M)
+    W, x, s = _setup(rng, 512, 768, max_bits, dtype, M=M)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128, 192, t)
+    pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
+    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, max_bits, 128, dtype), dtype, what=f"union M={M}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [2, 16, 40, 64, 65, 200])
+def test_reference_dispatch_dense_batches(M, dtype):
+    """Reference dispatch (grinqh/kernel.py:663-680): more than one row runs the
+    dense path regardless of thresholds; bias added in the activation dtype."""
+    rng = np.random.default_rng(100 + M)
+    b = 8
+    W, x, s = _setup(rng, 512, 512, b, dtype, M=M)
+    bias = to_dtype_np(rng.standard_normal(512), dtype)
+    x3 = x.reshape(1, M, 512)
+    y = torch.ops.grinqh.gemm_or_gemv(_tdt(x3, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128,
+                                      128, [5.0] * 4)
+    assert y.shape == (1, M, 512) and y.dtype == TORCH_DTYPES[dtype]
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    fin = O.dense_prefill(x, W, s, bias, 128, dtype)
+    assert_output_close(y.reshape(M, 512), pre, fin, dtype, bias=bias, what="dense dispatch",
+                        extra_tol=dense_rounding_bound(x, W, s, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(4096, 4096), (4096, 6144), (14336, 4096)])
+@pytest.mark.parametrize("M", [1, 16])
+def test_llama_shapes_graded(shape, M, dtype):
+    """Llama-3-8B linear shapes with the benchmark's synthetic recipe (1 %
+    outlier channels x20, thresholds 0/P50/P80/P95 of sigma), split-K active."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    K, N = shape
+    rng = np.random.default_rng(K + N + M)
+    W, x, s = _setup(rng, K, N, 8, dtype, M=M, scale_sd=0.01)
+    out = rng.permutation(K)[: math.ceil(K / 100)]
+    x = x.copy()
+    x[:, out] *= 20
+    x = to_dtype_np(x, dtype)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, 8), _tdt(s, dtype), None, 8, 128, N // 4, t)
+    pre = O.gemv_union_f64(x, W, s, t, 8, 128)
+    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, 8, 128, dtype), dtype, what=f"{shape} M={M}")
+
+
+def test_split_k_is_deterministic():
+    """Split-K partials are reduced in a fixed order: repeated calls are bitwise equal."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(5)
+    W, x, s = _setup(rng, 4096, 4096, 8, "float16", M=16, scale_sd=0.01)
+    P, xt, st = _prepare(W, 8), _tdt(x, "float16"), _tdt(s, "float16")
+    t = [0.0, 0.5, 1.0, 2.0]
+    y0 = grinqh_gemv_batch_union(xt, P, st, None, 8, 128, 1024, t)
+    for _ in range(3):
+        assert torch.equal(grinqh_gemv_batch_union(xt, P, st, None, 8, 128, 1024, t), y0)
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_nonfinite_rows_poison_their_output_row(M):
+    """A NaN or inf activation makes its whole output row NaN, as the
+    reference's sum of beta*x (0*NaN, 0*inf) does (grinqh/kernel.py:113-114)."""
+    rng = np.random.default_rng(6)
+    W, x, s = _setup(rng, 256, 256, 8, "float16", M=M)
+    x = x.copy()
+    x[0, 17] = np.nan
+    if M > 1:
+        x[M - 1, 200] = np.inf
+    xt = _tdt(x, "float16")
+    from grinqh.kernel import grinqh_gemv_batch_union
+    y = grinqh_gemv_batch_union(xt, _prepare(W, 8), _tdt(s, "float16"), None, 8, 128, 64, [0.1, 0.5, 1.0, 2.0])
+    y = y.float().cpu()
+    assert torch.isnan(y[0]).all()
+    if M > 1:
+        assert torch.isnan(y[M - 1]).all()
+        assert torch.isfinite(y[1]).all()
+
+
+def test_errors_are_raised_not_computed():
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(7)
+    W, x, s = _setup(rng, 256, 256, 8, "float16")
+    P = _prepare(W, 8)
+    with pytest.raises(ValueError):
+        grinqh_gemv_batch_union(_tdt(x, "float16"), P, _tdt(s, "float16"), None, 6, 128, 64, [0.0] * 4)
+    with pytest.raises(ValueError):
+        torch.ops.grinqh.gemm_or_gemv(torch.from_numpy(x).half(), P, _tdt(s, "float16"), None, 8, 128, 64, [0.0] * 4)
+    x48 = _tdt(rng.standard_normal((1, 48)), "float16")
+    with pytest.raises(ValueError):
+        torch.ops.grinqh.gemm_or_gemv(x48, P[:48], _tdt(s, "float16"), None, 8, 128, 64, [0.0] * 4)
+
+
+def test_graph_capture_replay_matches_eager():
+    """The op enqueues only kernels (no memset, no host sync): capture it in a
+    HIP graph and replay it several times with eager work in between."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(8)
+    W, x, s = _setup(rng, 4096, 4096, 8, "float16", M=4, scale_sd=0.01)
+    P, st = _prepare(W, 8), _tdt(s, "float16")
+    xin = _tdt(x, "float16")
+    t = [0.0, 0.5, 1.0, 2.0]
+    eager = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, 1024, t).clone()
+    g = torch.cuda.CUDAGraph()
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        grinqh_gemv_batch_union(xin, P, st, None, 8, 128, 1024, t)  # sizes this stream's workspace
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s_cap):
+            yg = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, 1024, t)
+    torch.cuda.current_stream().wait_stream(s_cap)
+    for i in range(4):
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, eager), f"replay {i}"
+        _ = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, 1024, t)
+        torch.cuda.synchronize()

@@ -1,0 +1,275 @@
+"""Pins for the CPU oracle (oracle/grinqh_oracle.py).
+
+Each check compares the oracle with something other than its own formula: the
+reference tests' identities (tests/test_grinqh_ops.py in the reference), an
+independent index derivation (the Marlin converter's address math,
+grinqh/kernel.py:393-398), closed forms, torch's own casts, and brute force.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import grinqh_oracle as O
+
+BITS = [2, 4, 6, 8]
+
+
+def _rand_w(rng, K, N, b):
+    lim = (1 << (b - 1)) - 1
+    return rng.integers(-lim - 1, lim + 1, size=(K, N), dtype=np.int64).astype(np.int8)
+
+
+# --------------------------------------------------------------------------- layout
+
+def test_preshuffle_index_formula_and_inverse():
+    rng = np.random.default_rng(1)
+    K, N = 5, 320
+    W = rng.integers(-128, 128, size=(K, N)).astype(np.int8)
+    P = O.preshuffle(W)
+    for c in range(N // 16):
+        for r in range(16):
+            assert np.array_equal(P[:, 16 * c + r], W[:, r * (N // 16) + c])
+    assert np.array_equal(O.postshuffle(P), W)
+    with pytest.raises(AssertionError):
+        O.preshuffle(np.zeros((2, 40), np.int8))
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_pack_unpack_roundtrip_and_size(b):
+    """tests/test_grinqh_ops.py:58-88 restated: storage = numel*b/8, per-row and
+    vectorised unpack equal, and unpack(pack(A)) == A >> (8-b)."""
+    rng = np.random.default_rng(b)
+    K, N = 384, 320
+    A = rng.integers(0, 256, size=(K, N), dtype=np.int64).astype(np.uint8)
+    B = O.pack_planes(A, b)
+    assert B.nbytes == A.size * b // 8
+    rec = np.stack([O.unpack_planes(B, i, b // 2, N // 4).view(np.uint8)[0] for i in range(K)])
+    vec = O.unpack_planes(B, np.arange(K), b // 2, N // 4).view(np.uint8)
+    assert np.array_equal(rec, vec)
+    assert np.array_equal(vec, A >> (8 - b))
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_plane_layout_matches_marlin_index_math(b):
+    """Independent derivation of S2+S4: the Marlin converter addresses logical
+    column n of row k at word (k, n % (N/16) [+ plane offset]) and bit
+    (lane%4)*8 + (3 - lane//4)*2 with lane = n // (N/16) (grinqh/kernel.py:393-412).
+    Assemble every code from those addresses and compare with W."""
+    rng = np.random.default_rng(10 + b)
+    K, N = 64, 256
+    W = _rand_w(rng, K, N, b)
+    B = O.prepare_weight(W, b)
+    Z = b // 2
+    ng = N // 16
+    n = np.arange(N)
+    grp = n % ng
+    lane = n // ng
+    shift = ((lane % 4) * 8 + (3 - lane // 4) * 2).astype(np.uint32)
+    code = np.zeros((K, N), np.int64)
+    for z in range(Z):
+        plane = B[:, z * ng + grp]
+        code = (code << 2) | ((plane >> shift[None, :]) & 3)
+    expect = W.astype(np.int64) & ((1 << b) - 1)
+    assert np.array_equal(code, expect)
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_decode_weight_inverts_prepare(b):
+    rng = np.random.default_rng(20 + b)
+    W = _rand_w(rng, 96, 160, b)
+    assert np.array_equal(O.decode_weight(O.prepare_weight(W, b), b, 160 // 4), W)
+
+
+# --------------------------------------------------------------------------- grading
+
+def test_grade_uses_fp32_threshold_and_strict_gt():
+    # t just below 1.0 in double rounds to 1.0 in fp32 -> |x| == 1.0 is NOT above it
+    t = [1.0 - 1e-12, 0.5, 2.0, -1.0]
+    bits = O.grade(np.array([1.0, -1.0, 0.75, np.nan, np.inf, -0.0], np.float16), t, 8)
+    assert [int(v) for v in bits] == [
+        0b1010, 0b1010, 0b1010, 0, 0b1111, 0b1000]
+    # numpy fp64 comparison would differ on the first element
+    assert 1.0 > t[0]
+
+
+def test_grade_bruteforce_all_fp16():
+    vals = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    t = [0.3, 1.7, 65504.0, 0.0]
+    bits = O.grade(vals, t, 8)
+    a = np.abs(vals.astype(np.float64))
+    for z, tz in enumerate(t):
+        tz32 = float(np.float32(tz))
+        with np.errstate(invalid="ignore"):
+            ok = a > tz32
+        assert np.array_equal(((bits >> z) & 1).astype(bool), ok)
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_grade_special_cases(b):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(256).astype(np.float16)
+    assert np.all(O.grade(x, [-1.0] * 4, b) == (1 << (b // 2)) - 1)
+    q1 = float(np.quantile(np.abs(x).astype(np.float32), 1.0))
+    assert np.all(O.grade(x, [q1] * 4, b) == 0)
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_effective_weight_prefix_closed_form(b):
+    """Prefix of `a` active zones keeps the top 2a bits and adds the midpoint of
+    the dropped bits: floor(c / 2^(b-2a)) * 2^(b-2a) + 2^(b-2a-1)."""
+    Z = b // 2
+    c = np.arange(-(1 << (b - 1)), 1 << (b - 1), dtype=np.int64)
+    W = c.astype(np.int8).reshape(-1, 1)
+    for a in range(Z + 1):
+        bits = np.full(W.shape[0], (1 << a) - 1, np.uint8)
+        got = O.effective_weight(W, bits, b)[:, 0]
+        if a == 0:
+            want = np.zeros_like(c)
+        elif a == Z:
+            want = c
+        else:
+            q = 1 << (b - 2 * a)
+            want = np.floor_divide(c, q) * q + q // 2
+        assert np.array_equal(got, want), a
+
+
+def test_effective_weight_nonprefix_mask_matches_reference_test_oracle():
+    """Non-monotone thresholds give non-prefix masks; restate the reference test
+    oracle literally (tests/test_grinqh_ops.py:36-55) with torch and compare."""
+    rng = np.random.default_rng(7)
+    for b in BITS:
+        W = _rand_w(rng, 64, 32, b)
+        x = rng.standard_normal((1, 64)).astype(np.float16)
+        t = [0.9, 0.1, 1.5, 0.0]
+        got = O.masked_weight_ref(W, x, t, b)
+
+        wt = torch.from_numpy(W)
+        xt = torch.from_numpy(x)
+        shift_amt = 8 - b
+        x_abs = xt.abs().float().flatten()
+        w_u8 = (wt << shift_amt).view(torch.uint8)
+        row_mask = torch.zeros_like(x_abs, dtype=torch.uint8)
+        bias = torch.zeros_like(x_abs, dtype=torch.float32)
+        prev = 0
+        for zone in range(b // 2):
+            active = x_abs > t[zone]
+            row_mask |= active.to(torch.uint8) * (0xC0 >> 2 * zone)
+            cur = (1 << (b - 1)) >> (2 * zone + 2)
+            bias += active * (cur - prev)
+            prev = cur
+        ref = (w_u8 & row_mask[:, None]).view(torch.int8).float() / 2 ** shift_amt + bias[:, None]
+        assert np.array_equal(got, ref.double().numpy())
+
+
+# --------------------------------------------------------------------------- products
+
+def test_bf16_cast_matches_torch():
+    rng = np.random.default_rng(4)
+    y = np.concatenate([rng.standard_normal(10000) * 10.0 ** rng.integers(-6, 6, 10000),
+                        [0.0, -0.0, np.inf, -np.inf, 3.0e38]])
+    ours = O.rne_cast(y, "bfloat16")
+    ref = torch.from_numpy(y.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(ours, ref)
+    ours16 = O.rne_cast(y, "float16")
+    ref16 = torch.from_numpy(y.astype(np.float32)).half().double().numpy()
+    assert np.array_equal(ours16, ref16)
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_gemv_all_active_is_dense_fp32(b):
+    """tests/test_grinqh_ops.py:156-190: thresholds -1 -> the GEMV equals
+    X @ (W * s) (fp32 in the reference; float64 here)."""
+    rng = np.random.default_rng(5)
+    W = _rand_w(rng, 256, 256, b)
+    x = rng.standard_normal((1, 256)).astype(np.float16)
+    s = rng.standard_normal((2, 256)).astype(np.float16)
+    y = O.gemv_f64(x, W, s, [-1.0] * 4, b, 128)
+    ref = x.astype(np.float64) @ (W.astype(np.float64) * np.repeat(s.astype(np.float64), 128, 0))
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-9)
+
+
+@pytest.mark.parametrize("b", BITS)
+def test_gemv_skip_all_is_zero(b):
+    rng = np.random.default_rng(6)
+    W = _rand_w(rng, 256, 256, b)
+    x = rng.standard_normal((1, 256)).astype(np.float16)
+    s = rng.standard_normal((2, 256)).astype(np.float16)
+    q = float(np.quantile(np.abs(x).astype(np.float32), 1.0))
+    y = O.gemv(x, W, s, None, [q] * 4, b, 128)
+    assert np.all(y == 0)
+
+
+def test_gemv_bruteforce_tiny():
+    """Brute-force S8 element by element from the zone rule on a tiny case."""
+    rng = np.random.default_rng(8)
+    b, K, N = 8, 32, 16
+    W = _rand_w(rng, K, N, b)
+    x = rng.standard_normal((1, K)).astype(np.float16)
+    s = (rng.random((1, N)) + 0.5).astype(np.float16)
+    t = [0.2, 0.6, 1.1, 1.9]
+    y = O.gemv_f64(x, W, s, t, b, 128)
+    for n in range(N):
+        acc = 0.0
+        for k in range(K):
+            xv = float(x[0, k])
+            a = sum(1 for z in range(4) if np.float32(abs(xv)) > np.float32(t[z]))
+            prefix = all(np.float32(abs(xv)) > np.float32(t[z]) for z in range(a))
+            assert prefix  # thresholds are increasing here
+            c = int(W[k, n])
+            if a == 0:
+                w = 0
+            elif a == 4:
+                w = c
+            else:
+                q = 1 << (8 - 2 * a)
+                w = (c // q) * q + q // 2
+            acc += xv * w * float(s[0, n])
+        assert abs(acc - y[0, n]) <= 1e-9 * max(1.0, abs(acc))
+
+
+@pytest.mark.parametrize("b", BITS)
+@pytest.mark.parametrize("B", [2, 3, 5, 8])
+def test_union_identities(b, B):
+    """tests/test_grinqh_ops.py:245-282: at all-active thresholds the union GEMV
+    equals the looped per-row GEMV and the dense masked reference."""
+    rng = np.random.default_rng(9)
+    W = _rand_w(rng, 256, 256, b)
+    x = rng.standard_normal((B, 256)).astype(np.float16)
+    s = rng.standard_normal((2, 256)).astype(np.float16)
+    t = [-1.0] * 4
+    yu = O.gemv_union_f64(x, W, s, t, b, 128)
+    yl = np.concatenate([O.gemv_f64(x[i:i + 1], W, s, t, b, 128) for i in range(B)])
+    np.testing.assert_allclose(yu, yl, rtol=1e-12, atol=1e-9)
+    # the union statistic is the column max of |x|
+    tq = [0.5, 1.0, 1.5, 2.0]
+    bits_u = O.grade(np.abs(x.astype(np.float32)).max(0), tq, b)
+    wm = O.effective_weight(W, bits_u, b).astype(np.float64)
+    ref = x.astype(np.float64) @ (wm * np.repeat(s.astype(np.float64), 128, 0))
+    np.testing.assert_allclose(O.gemv_union_f64(x, W, s, tq, b, 128), ref, rtol=1e-12, atol=1e-9)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("b", BITS)
+def test_dense_weight_elementwise_rne(dtype, b):
+    """S9 elementwise W*s rounded in the activation dtype, checked against
+    torch's own CPU multiply in that dtype (tests/test_grinqh_ops.py:106)."""
+    rng = np.random.default_rng(11)
+    W = _rand_w(rng, 256, 64, b)
+    s = rng.standard_normal((2, 64)).astype(np.float32)
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    st = torch.from_numpy(s).to(tdt)
+    ref = (torch.from_numpy(W).to(tdt) * st.repeat_interleave(128, 0)).double().numpy()
+    got = O.dense_weight(W, st.double().numpy(), 128, dtype)
+    assert np.array_equal(got, ref)
+
+
+def test_dispatch_shapes():
+    rng = np.random.default_rng(12)
+    W = _rand_w(rng, 128, 64, 8)
+    s = rng.standard_normal((1, 64)).astype(np.float16)
+    x = rng.standard_normal((2, 3, 128)).astype(np.float16)
+    y = O.gemm_or_gemv(x, W, s, None, 8, 128, [0.1] * 4)
+    assert y.shape == (2, 3, 64)
+    np.testing.assert_array_equal(y.reshape(6, 64), O.dense_prefill(x.reshape(6, 128), W, s, None, 128))
+    y1 = O.gemm_or_gemv(x[:1, :1], W, s, None, 8, 128, [0.1] * 4)
+    np.testing.assert_array_equal(y1.reshape(1, 64), O.gemv(x[0, :1], W, s, None, [0.1] * 4, 8, 128))

@@ -1,0 +1,209 @@
+// extern "C" entry points of libgrinqh_hip.so (declared in include/grinqh.h):
+// argument validation, workspace carving and kernel selection.
+#include <string.h>
+
+#include "grinqh_common.h"
+#include "grinqh_launch.h"
+
+using namespace grinqh;
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+constexpr int64_t kDecodeMaxRows = 64;  // rows handled by one decode launch
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool valid_bits(int b) { return b == 2 || b == 4 || b == 6 || b == 8; }
+inline bool valid_dtype(int d) { return d == GRINQH_DTYPE_F16 || d == GRINQH_DTYPE_BF16; }
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct WorkspaceLayout {
+  size_t sigma_off, partial_off, total;
+  DecodePlan plan;
+};
+
+// [counters | sigma (K floats, union batches split into several launches) | split-K partials]
+WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
+  WorkspaceLayout w{};
+  const int64_t m_launch = M < kDecodeMaxRows ? M : kDecodeMaxRows;
+  w.plan = plan_decode(m_launch > 0 ? m_launch : 1, K, N);
+  size_t partial = w.plan.splits > 1 ? w.plan.workspace - kCounterBytes : 0;
+  if (M > kDecodeMaxRows && M % kDecodeMaxRows != 0) {  // the last, shorter launch may split differently
+    const DecodePlan tail = plan_decode(M % kDecodeMaxRows, K, N);
+    const size_t tail_partial = tail.splits > 1 ? tail.workspace - kCounterBytes : 0;
+    if (tail_partial > partial) partial = tail_partial;
+  }
+  const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kDecodeMaxRows;
+  w.sigma_off = kCounterBytes;
+  w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
+  w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
+  return w;
+}
+
+int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                       const void* planes, const void* scale, void* y, int max_bits, int group_size) {
+  if (!valid_dtype(dtype) || !valid_bits(max_bits)) return GRINQH_ERR_INVALID;
+  if (M < 0 || K <= 0 || N <= 0 || K % 32 != 0 || N % 16 != 0) return GRINQH_ERR_INVALID;
+  if (group_size <= 0 || group_size % 32 != 0) return GRINQH_ERR_INVALID;
+  if (K > (int64_t)1 << 30 || N > (int64_t)1 << 24 || M > (int64_t)1 << 30) return GRINQH_ERR_INVALID;
+  if (M > 0 && (x == nullptr || planes == nullptr || scale == nullptr || y == nullptr)) return GRINQH_ERR_INVALID;
+  if (ldx < K || ldx % 8 != 0 || !aligned(x, 16) || !aligned(planes, 4)) return GRINQH_ERR_INVALID;
+  if ((N / 16 + 15) / 16 > kMaxCounters) return GRINQH_ERR_INVALID;
+  return GRINQH_OK;
+}
+
+int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, const void* planes,
+                const void* scale, const void* bias, void* y, int max_bits, int group_size,
+                const float* thresholds, int mode, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = check_product_args(x, M, K, ldx, N, dtype, planes, scale, y, max_bits, group_size);
+  if (rc != GRINQH_OK) return rc;
+  if (mode != GRINQH_MODE_REFERENCE && mode != GRINQH_MODE_UNION && mode != GRINQH_MODE_DENSE)
+    return GRINQH_ERR_INVALID;
+  if (M == 0) return GRINQH_OK;
+  const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
+  if (graded && thresholds == nullptr) return GRINQH_ERR_INVALID;
+
+  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE);
+  if (wl.total > 0 && (workspace == nullptr || ws_bytes < wl.total || !aligned(workspace, 256)))
+    return GRINQH_ERR_WORKSPACE;
+  hipStream_t st = as_stream(stream);
+  char* ws = static_cast<char*>(workspace);
+
+  DecodeParams p{};
+  p.planes = static_cast<const uint32_t*>(planes);
+  p.scale = static_cast<const uint16_t*>(scale);
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.ldx = ldx;
+  p.K = (int)K;
+  p.N = (int)N;
+  p.NW = (int)(N / 16);
+  p.gs = group_size;
+  for (int i = 0; i < 4; ++i) p.thr.t[i] = graded ? thresholds[i] : 0.f;
+  p.counters = reinterpret_cast<unsigned*>(ws);
+  p.partial = ws ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
+  p.sigma = nullptr;
+
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  uint16_t* ys = static_cast<uint16_t*>(y);
+  if (graded && M > kDecodeMaxRows) {
+    float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
+    rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sigma, st);
+    if (rc != GRINQH_OK) return rc;
+    p.sigma = sigma;
+  }
+  for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
+    const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
+    const DecodePlan plan = plan_decode(mc, K, N);
+    p.x = xs + m0 * ldx;
+    p.y = ys + m0 * N;
+    p.M = (int)mc;
+    p.splits = plan.splits;
+    p.tiles_per_split = plan.tiles_per_split;
+    rc = launch_decode(p, plan, max_bits, dtype, !graded, st);
+    if (rc != GRINQH_OK) return rc;
+  }
+  return GRINQH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int grinqh_abi_version(void) { return kAbiVersion; }
+
+const char* grinqh_status_string(int status) {
+  switch (status) {
+    case GRINQH_OK: return "ok";
+    case GRINQH_ERR_INVALID: return "invalid argument (shape, dtype, bit width, alignment or mode)";
+    case GRINQH_ERR_HIP: return "HIP kernel launch failed";
+    case GRINQH_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
+    default: return "unknown status";
+  }
+}
+
+int grinqh_pack_planes(const void* codes_u8, void* planes_u32, int64_t K, int64_t N, int max_bits,
+                       void* stream) {
+  if (!valid_bits(max_bits) || K < 0 || N < 0 || N % 16 != 0) return GRINQH_ERR_INVALID;
+  if (K * N == 0) return GRINQH_OK;
+  if (codes_u8 == nullptr || planes_u32 == nullptr || !aligned(codes_u8, 16) || !aligned(planes_u32, 4))
+    return GRINQH_ERR_INVALID;
+  if (K > INT32_MAX || N > INT32_MAX) return GRINQH_ERR_INVALID;
+  return launch_pack_planes(static_cast<const uint32_t*>(codes_u8), static_cast<uint32_t*>(planes_u32), (int)K,
+                            (int)N, max_bits, as_stream(stream));
+}
+
+int grinqh_prepare_weight(const void* w_int8, void* planes_u32, int64_t K, int64_t N, int max_bits,
+                          void* stream) {
+  if (!valid_bits(max_bits) || K < 0 || N < 0 || N % 16 != 0) return GRINQH_ERR_INVALID;
+  if (K * N == 0) return GRINQH_OK;
+  if (w_int8 == nullptr || planes_u32 == nullptr || !aligned(planes_u32, 4)) return GRINQH_ERR_INVALID;
+  if (K > INT32_MAX || N > INT32_MAX) return GRINQH_ERR_INVALID;
+  return launch_prepare_weight(static_cast<const int8_t*>(w_int8), static_cast<uint32_t*>(planes_u32), (int)K,
+                               (int)N, max_bits, as_stream(stream));
+}
+
+int grinqh_unpack_planes(const void* planes_u32, const int64_t* rows, int64_t n_rows, void* codes_u32, int64_t K,
+                         int64_t N, int bit_level, void* stream) {
+  if (bit_level < 1 || bit_level > 4 || n_rows < 0 || K < 0 || N < 0 || N % 16 != 0) return GRINQH_ERR_INVALID;
+  if (n_rows * N == 0) return GRINQH_OK;
+  if (planes_u32 == nullptr || rows == nullptr || codes_u32 == nullptr || !aligned(codes_u32, 16))
+    return GRINQH_ERR_INVALID;
+  if (n_rows > INT32_MAX || N > INT32_MAX) return GRINQH_ERR_INVALID;
+  return launch_unpack_planes(static_cast<const uint32_t*>(planes_u32), rows, static_cast<uint32_t*>(codes_u32),
+                              (int)n_rows, (int)N, bit_level, as_stream(stream));
+}
+
+int grinqh_dequantize(const void* planes_u32, const void* scale, void* out, int64_t K, int64_t N, int max_bits,
+                      int group_size, int dtype, void* stream) {
+  if (!valid_bits(max_bits) || !valid_dtype(dtype) || K < 0 || N < 0 || N % 16 != 0) return GRINQH_ERR_INVALID;
+  if (scale != nullptr && group_size <= 0) return GRINQH_ERR_INVALID;
+  if (K * N == 0) return GRINQH_OK;
+  if (planes_u32 == nullptr || out == nullptr) return GRINQH_ERR_INVALID;
+  if (K > INT32_MAX || N > INT32_MAX) return GRINQH_ERR_INVALID;
+  return launch_dequant(static_cast<const uint32_t*>(planes_u32), static_cast<const uint16_t*>(scale), out, (int)K,
+                        (int)N, max_bits, group_size > 0 ? group_size : 1, dtype, as_stream(stream));
+}
+
+int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, int max_bits,
+                 const float thresholds[4], uint8_t* zone_bits, int32_t* beta, void* stream) {
+  if (!valid_bits(max_bits) || !valid_dtype(dtype) || M < 1 || K < 0 || ldx < K) return GRINQH_ERR_INVALID;
+  if (K == 0) return GRINQH_OK;
+  if (x == nullptr || thresholds == nullptr || zone_bits == nullptr) return GRINQH_ERR_INVALID;
+  if (K > INT32_MAX || M > INT32_MAX) return GRINQH_ERR_INVALID;
+  return launch_grade(static_cast<const uint16_t*>(x), ldx, (int)M, (int)K, thresholds, max_bits, dtype, zone_bits,
+                      beta, as_stream(stream));
+}
+
+size_t grinqh_workspace_bytes(int64_t M, int64_t K, int64_t N, int max_bits, int mode) {
+  (void)max_bits;
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
+  return layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE).total;
+}
+
+int grinqh_gemm_or_gemv(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                        const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
+                        int group_size, const float thresholds[4], int mode, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds, mode,
+                     workspace, workspace_bytes, stream);
+}
+
+int grinqh_gemv_batch_union(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                            const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
+                            int group_size, const float thresholds[4], void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds,
+                     GRINQH_MODE_UNION, workspace, workspace_bytes, stream);
+}
+
+int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                         const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
+                         int group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, nullptr,
+                     GRINQH_MODE_DENSE, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

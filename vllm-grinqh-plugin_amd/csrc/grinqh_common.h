@@ -1,0 +1,156 @@
+// Shared device helpers for the GRINQH gfx950 kernels.
+//
+// Weight layout (identical bytes to the reference's packed parameter, produced
+// by process_weights_after_loading in grinqh/grinqh.py:200-210 of the
+// reference): uint32 planes[K][Z][NW] with NW = N/16.  Word (k, z, c) holds,
+// in byte beta / slot j (bits 8*beta+7-2j .. 8*beta+6-2j), the 2-bit digit z
+// (most significant first) of logical column n = (4j+beta)*NW + c of row k.
+//
+// A lane that owns word column c therefore sees 16 logical columns at once,
+// one per "column tile" r = 4j+beta; tile r of a 16-word block w0..w0+15 is the
+// 16 contiguous columns r*NW + w0 .. r*NW + w0 + 15.  This is what maps the
+// plane words straight onto the B operand of v_mfma_f32_16x16x32_{f16,bf16}
+// (lane = column-in-tile + 16*k_octet, 8 consecutive k per lane).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace grinqh {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+struct F16 { static constexpr int id = 0; };
+struct BF16 { static constexpr int id = 1; };
+
+// ---------------------------------------------------------------- scalars
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  _Float16 v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  uint16_t h;
+  __builtin_memcpy(&h, &v, 2);
+  return h;
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
+  return (uint16_t)(u >> 16);
+}
+
+template <typename DT> __device__ __forceinline__ float to_f32(uint16_t h);
+template <> __device__ __forceinline__ float to_f32<F16>(uint16_t h) { return f16_bits_to_f32(h); }
+template <> __device__ __forceinline__ float to_f32<BF16>(uint16_t h) { return bf16_bits_to_f32(h); }
+template <typename DT> __device__ __forceinline__ uint16_t from_f32(float f);
+template <> __device__ __forceinline__ uint16_t from_f32<F16>(float f) { return f32_to_f16_bits(f); }
+template <> __device__ __forceinline__ uint16_t from_f32<BF16>(float f) { return f32_to_bf16_bits(f); }
+
+// Output epilogue shared by every product kernel: the reference casts the fp32
+// result to the activation dtype and then adds the bias in that dtype
+// (grinqh/kernel.py:706-708), i.e. two roundings.
+template <typename DT>
+__device__ __forceinline__ uint16_t finish_output(float acc, const uint16_t* bias, int n) {
+  uint16_t y = from_f32<DT>(acc);
+  if (bias != nullptr) y = from_f32<DT>(to_f32<DT>(y) + to_f32<DT>(bias[n]));
+  return y;
+}
+
+// ---------------------------------------------------------------- bytes
+
+// v_perm_b32: byte selector 0..3 picks from `lo`, 4..7 from `hi`, 0x0c gives 0.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+__device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t r) {
+  return __builtin_amdgcn_alignbit(v, v, r);
+}
+
+// ---------------------------------------------------------------- MFMA
+
+template <typename DT>
+__device__ __forceinline__ f32x4_t mfma16x16x32(const u32x4_t& a, const u32x4_t& b, f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x32<F16>(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x32<BF16>(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- grading
+
+// sigma_k = max_m |x[m][k]| with NaN ignored (fmaxf) unless every entry is NaN.
+// Loads are issued in batches of 8 independent, clamped (in-bounds) addresses.
+template <typename DT>
+__device__ __forceinline__ float column_absmax(const uint16_t* __restrict__ x, int64_t ldx, int M, int k) {
+  float s = fabsf(to_f32<DT>(x[k]));
+  for (int m0 = 1; m0 < M; m0 += 8) {
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = x[(int64_t)min(m0 + i, M - 1) * ldx + k];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = fmaxf(s, fabsf(to_f32<DT>(v[i])));
+  }
+  return s;
+}
+
+
+// Zone bits of one row statistic: bit z set iff z < Z and fp32(|sigma|) > t_z
+// (strict, NaN false), the Triton fp32 promotion of grinqh/kernel.py:100-106.
+template <int Z>
+__device__ __forceinline__ uint32_t zone_bits(float sigma_abs, const float* thr) {
+  uint32_t b = 0;
+#pragma unroll
+  for (int z = 0; z < Z; ++z) b |= (sigma_abs > thr[z]) ? (1u << z) : 0u;
+  return b;
+}
+
+// Midpoint bias beta of an arbitrary zone set: sum of the telescoped deltas
+// Delta_0 = B>>2, Delta_z = (B>>(2z+2)) - (B>>2z), B = 1<<(b-1)
+// (grinqh/kernel.py:73-82, 108-113).
+template <int Z>
+__device__ __forceinline__ int midpoint_bias(uint32_t bits) {
+  constexpr int B = 1 << (2 * Z - 1);
+  int beta = 0, prev = 0;
+#pragma unroll
+  for (int z = 0; z < Z; ++z) {
+    const int cur = B >> (2 * z + 2);
+    if ((bits >> z) & 1u) beta += cur - prev;
+    prev = cur;
+  }
+  return beta;
+}
+
+// ---------------------------------------------------------------- unpack
+
+// Rebuild the masked code bytes V_j (one byte per column tile 4j+beta) of one
+// row from its plane words D[z]; planes that are inactive for the row must be
+// passed as 0.  The result is (U & mask) with U = code << (8-b), XOR 0x80 in
+// every byte when zone 0 is active, i.e. offset-binary int8(U & mask) + 128.
+// Bits 8b+6-2j of D[z] move to 8b+6-2z: a rotation by 2(z-j) mod 32.
+template <int Z>
+__device__ __forceinline__ uint32_t rebuild_dword(const uint32_t (&D)[Z], uint32_t init, int j) {
+  uint32_t v = init;
+#pragma unroll
+  for (int z = 0; z < Z; ++z) {
+    const uint32_t m = 0xC0C0C0C0u >> (2 * z);
+    v ^= rotr(D[z], (uint32_t)(2 * (z - j)) & 31u) & m;
+  }
+  return v;
+}
+
+}  // namespace grinqh

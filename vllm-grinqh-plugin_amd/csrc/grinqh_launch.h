@@ -1,0 +1,73 @@
+// Internal launch interface between the C ABI (capi.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "grinqh.h"
+
+namespace grinqh {
+
+struct GradeThresholds {
+  float t[4];
+};
+
+// Counters live in the first kCounterBytes of the workspace.
+constexpr size_t kCounterBytes = 4096;
+constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(unsigned));
+// Upper bound on the split-K partial-sum area.
+constexpr size_t kMaxPartialBytes = size_t(64) << 20;
+
+struct DecodeParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint32_t* planes;
+  const uint16_t* scale;
+  const uint16_t* bias;
+  uint16_t* y;
+  GradeThresholds thr;
+  int M, K, N, NW, gs;
+  int splits;           // grid.y: K ranges
+  int tiles_per_split;  // 32-row tiles per K range
+  float* partial;       // [splits][M][N] fp32 when splits > 1
+  unsigned* counters;   // [grid.x] arrival counters when splits > 1
+  const float* sigma;   // optional precomputed union statistic [K] (else computed from x)
+};
+
+struct DecodePlan {
+  int mt;      // 16-row m-tiles: 1, 2 or 4 (M <= 16, 32, 64)
+  int splits;
+  int tiles_per_split;
+  int col_blocks;
+  size_t workspace;  // bytes incl. counters, 0 if splits == 1
+};
+
+DecodePlan plan_decode(int64_t M, int64_t K, int64_t N);
+
+int launch_decode(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense,
+                  hipStream_t st);
+int launch_sigma(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* sigma, hipStream_t st);
+
+struct PrefillParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint32_t* planes;
+  const uint16_t* scale;
+  const uint16_t* bias;
+  uint16_t* y;
+  GradeThresholds thr;
+  int M, K, N, NW, gs;
+};
+
+int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st);
+
+int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
+int launch_prepare_weight(const int8_t* W, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
+int launch_unpack_planes(const uint32_t* P, const int64_t* rows, uint32_t* out, int n_rows, int N, int Z,
+                         hipStream_t st);
+int launch_dequant(const uint32_t* P, const uint16_t* scale, void* out, int K, int N, int max_bits, int gs,
+                   int dtype, hipStream_t st);
+int launch_grade(const uint16_t* x, int64_t ldx, int M, int K, const float* t, int max_bits, int dtype,
+                 uint8_t* bits, int32_t* beta, hipStream_t st);
+
+}  // namespace grinqh
