@@ -51,6 +51,8 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
   if (M > 0 && (x == nullptr || planes == nullptr || scale == nullptr || y == nullptr)) return GRINQH_ERR_INVALID;
   if (ldx < K || ldx % 8 != 0 || !aligned(x, 16) || !aligned(planes, 4)) return GRINQH_ERR_INVALID;
   if ((N / 16 + 15) / 16 > kMaxCounters) return GRINQH_ERR_INVALID;
+  // plane words are addressed with 32-bit byte offsets (bit 31 reserved)
+  if (K * (max_bits / 2) * (N / 16) * 4 >= ((int64_t)1 << 31)) return GRINQH_ERR_INVALID;
   return GRINQH_OK;
 }
 

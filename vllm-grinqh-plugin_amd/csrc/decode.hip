@@ -12,18 +12,25 @@
 //   grid.y  = K range of `tiles_per_split` 32-row tiles (split-K)
 //   4 waves = MT groups of output dwords j x (4/MT) K sub-ranges
 //
-// Per 32-row tile each lane (c = lane&15, q = lane>>4) owns rows 8q..8q+7 of
-// word column c.  It loads, for every plane z active in a row, one 32-bit
-// plane word (predicated per row, so only the planes a row needs are fetched),
-// rebuilds the masked code bytes of its 16 columns with rotate+mask, and turns
-// row pairs into the MFMA B operand:
+// Phase 1 (whole block): stage x[:, K range] in LDS, grade every row (sigma =
+// max_m |x|, zone bits, midpoint bias) and precompute each (row, plane) byte
+// offset, with bit 31 set for planes the row does not need.
+//
+// Phase 2 (per wave): for each tile, each lane (c = lane&15, q = lane>>4) loads
+// one 32-bit plane word per (row, plane) of its 8 rows with raw buffer loads;
+// offsets with bit 31 set fall past the buffer end and return 0 without a
+// memory access, so only the planes a row needs are fetched and no load is
+// branched around.  Two tiles of loads stay in flight while the current tile
+// is unpacked (one wave per SIMD, 512 registers).  Code bytes are rebuilt
+// branch-free: G_z = rot(D_z, 2z), H_j = field merge of the G_z,
+// V_j = rot(H_j, -2j); then turned into the MFMA B operand:
 //   fp16: 0x64 | byte  -> 1024 + u exactly     (u = offset-binary code)
 //   bf16: cvt_f32_ubyte, upper half            -> u exactly
 // The constant offset and the midpoint bias beta are removed by one extra MFMA
 // per tile whose B operand is the per-row value beta*2^sh - off (a "correction
-// column" shared by all 16 columns), so per scale group
-//   y += s[g][n] * 2^-sh * (C[m][n] + Cv[m]).
-// Scales are applied per 128-row group in fp32 as in grinqh/kernel.py:148-158.
+// column" shared by all 16 columns); per scale group
+//   y += s[g][n] * 2^-sh * (C[m][n] + Cv[m])
+// in fp32, as grinqh/kernel.py:148-158 applies scales.
 //
 // Split-K partials are reduced deterministically: the 4/MT waves of a block
 // through LDS in fixed order, the K ranges by the last-arriving block (fixed
@@ -33,7 +40,7 @@
 
 namespace grinqh {
 
-constexpr int kDecodeRowsMax = 8192;  // rows graded per block (LDS: 3 bytes per row)
+constexpr int kDecodeRowsPerBlock = 1024;  // rows per block at MT = 1 (x staged in LDS)
 
 template <typename DT>
 struct BOperand;
@@ -73,18 +80,34 @@ struct BOperand<BF16> {
 };
 
 template <typename DT, int MT, int Z, bool DENSE>
-__global__ __launch_bounds__(256, 2) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
+  constexpr int MP = 16 * MT;  // padded rows of x
   constexpr int NJ = 4 / MT;   // output dwords j per wave
   constexpr int KW = 4 / MT;   // K sub-ranges per block
   constexpr int SH = 8 - 2 * Z;
-  constexpr int NRED = (KW - 1) * MT > 0 ? (KW - 1) * MT : 1;
+  constexpr int RMAX = kDecodeRowsPerBlock / MT;
+  constexpr int XS = RMAX + 8;  // halves per staged x row (16-byte rows, banks staggered)
+  constexpr int X_BYTES = MP * XS * 2;
+  constexpr int OFF_BYTES = RMAX * Z * 4;
+  constexpr int RED_VECS = (KW - 1) * MT * 16 * 64;  // f32x4 slots for the in-block reduction
+  constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_VECS * 16 ? (X_BYTES + OFF_BYTES) : RED_VECS * 16;
+  constexpr int SC_GROUPS = RMAX / 32 + 1;  // scale groups a K range can touch (group size >= 32)
+  constexpr int CPR = RMAX / 8;             // 16-byte x chunks per staged row
+  constexpr int XPT = MP * CPR / 256;       // x chunks per thread
+  constexpr int SPT = (SC_GROUPS * 32 + 255) / 256;  // 16-byte scale chunks per thread
 
-  __shared__ __align__(16) uint8_t s_bits[kDecodeRowsMax];
-  __shared__ __align__(16) uint16_t s_bv[kDecodeRowsMax];
-  __shared__ f32x4_t s_red[NRED * 16 * 64];
+  // staging area: x rows and (row, plane) offsets; reused for the in-block reduction
+  __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
+  __shared__ __align__(16) uint8_t s_bits[RMAX];   // row -> zone bits
+  __shared__ __align__(16) uint16_t s_bv[RMAX];    // row -> correction-column value
+  __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
   __shared__ int s_last;
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
+  uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
+  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(s_pool);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int jg = wave % MT, kw = wave / MT;
   const int c = lane & 15, q = lane >> 4;
   const int w0 = blockIdx.x * 16;
@@ -93,26 +116,87 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeParams p) {
   const int tile0 = split * p.tiles_per_split;
   const int tile1 = min(tile0 + p.tiles_per_split, ntiles_total);
   const int nt = tile1 - tile0;
+  const int R = nt * 32;
   const int row0 = tile0 * 32;
+  const int g_first = row0 / p.gs;
+  const int n_groups = (row0 + R - 1) / p.gs - g_first + 1;
 
-  // ---- phase 1: grade the block's rows (zone bits + correction-column value)
-  for (int rr = tid; rr < nt * 32; rr += 256) {
-    const int k = row0 + rr;
+  // ---- phase 1a: stage x[:, row0 .. row0+R) and the scales in LDS, all loads in flight at once.
+  // Out-of-range buffer offsets read 0: rows m >= M stage as zeros, and nothing past the end of
+  // x or the scale array is touched.
+  {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
+    const uint32_t sbytes = (uint32_t)((uint64_t)((p.K + p.gs - 1) / p.gs) * p.N * 2u);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.scale), (short)0, (int)sbytes, 0x00020000);
+    const int u = tid % CPR, mb = tid / CPR;
+    u32x4_t xv[XPT];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int m = mb + k * (256 / CPR);
+      const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
+      xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+    }
+    const bool vec_scales = (p.NW % 8) == 0;
+    u32x4_t sv[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + 256 * k;  // (group, tile, half) chunk
+      const int gl = h >> 5, r = (h >> 1) & 15, hf = h & 1;
+      const uint32_t off =
+          (gl < n_groups && vec_scales)
+              ? (uint32_t)(((int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + w0 + 8 * hf) * 2)
+              : 0x80000000u;
+      sv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(sr, (int)off, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int m = mb + k * (256 / CPR);
+      *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + 256 * k;
+      if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
+    }
+    if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
+      for (int idx = tid; idx < n_groups * 256; idx += 256) {
+        const int gl = idx >> 8, col = idx & 255;
+        const int wcol = min(w0 + (col & 15), p.NW - 1);
+        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)(col >> 4) * p.NW + wcol];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 1b: grade each row: zone bits, correction-column value, plane offsets
+  for (int rr = tid; rr < R; rr += 256) {
     uint32_t bits;
     if (DENSE) {
       bits = (1u << Z) - 1u;
     } else {
-      const float s = p.sigma != nullptr ? p.sigma[k] : column_absmax<DT>(p.x, p.ldx, p.M, k);
+      float s;
+      if (p.sigma != nullptr) {
+        s = p.sigma[row0 + rr];
+      } else {
+        s = fabsf(to_f32<DT>(s_x[rr]));
+        for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
+      }
       bits = zone_bits<Z>(s, p.thr.t);
     }
     s_bits[rr] = (uint8_t)bits;
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
     const float off = BOperand<DT>::kBase + ((bits & 1u) ? 128.f : 0.f);
     s_bv[rr] = from_f32<DT>((float)(beta * (1 << SH)) - off);
+    const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
+#pragma unroll
+    for (int z = 0; z < Z; ++z)
+      s_off[rr * Z + z] = ((bits >> z) & 1u) ? row_bytes + (uint32_t)z * (uint32_t)p.NW * 4u : 0x80000000u;
   }
   __syncthreads();
 
-  // ---- phase 2: main loop over this wave's tiles, one scale group at a time
+  // ---- phase 2: main loop over this wave's tiles
   f32x4_t Y[MT][NJ][4];
   f32x4_t C[MT][NJ][4];
   f32x4_t Cv[MT];
@@ -123,150 +207,192 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) Y[mt][jj][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // Lanes past the last word column read the last valid column instead (their
+  // outputs are never stored), so every address below is in bounds.
   const bool col_ok = (w0 + c) < p.NW;
-  const int wc = col_ok ? (w0 + c) : (p.NW - 1);  // clamped word column: loads stay in bounds
-  const int64_t rstride = (int64_t)Z * p.NW;
-  const uint32_t* pbase = p.planes + wc;
+  const int wc = col_ok ? (w0 + c) : (p.NW - 1);
   const float post = 1.0f / (float)(1 << SH);
   const int t_begin = (nt * kw) / KW, t_end = (nt * (kw + 1)) / KW;
   const int tiles_per_group = p.gs >> 5;
-  // rows of the A operand: m = 16*mt + c, clamped so every load is in bounds
-  // (rows >= M only feed output rows that are never written)
-  const uint16_t* xrow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = p.x + (int64_t)min(16 * mt + c, p.M - 1) * p.ldx + 8 * q;
 
-  for (int t = t_begin; t < t_end;) {
-    const int g = (row0 + 32 * t) / p.gs;
-    const int t_stop = min(t_end, (g + 1) * tiles_per_group - tile0);
-    // prefetch this group's scales (independent loads, consumed after the tiles)
-    uint16_t sraw[NJ][4];
+  // Plane words come from raw buffer loads: a (row, plane) a lane does not
+  // need has offset bit 31 set, past the buffer end, which returns 0 without a
+  // memory access.  The main loop issues every load unconditionally (tiles past
+  // the end of the range are entirely out of bounds), so wait counts stay
+  // static and two prefetched tiles remain in flight.
+  const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(p.planes), (short)0, (int)((uint64_t)p.K * (uint32_t)(Z * p.NW) * 4u), 0x00020000);
+  const uint32_t lane_off = (uint32_t)wc * 4u;
+
+  typedef uint32_t offz_t __attribute__((ext_vector_type(Z)));
+  auto issue = [&](int t, uint32_t (&D)[8][Z], u32x2_t& mb) {
+    const bool live = t < t_end;
+    const int sb = (live ? t : t_begin) * 32 + 8 * q;
+    mb = *reinterpret_cast<const u32x2_t*>(&s_bits[sb]);
+    const uint32_t dead = live ? 0u : 0x80000000u;
 #pragma unroll
-    for (int jj = 0; jj < NJ; ++jj)
+    for (int e = 0; e < 8; ++e) {
+      offz_t o;
+      if constexpr (Z == 1) {
+        o = s_off[sb + e];
+      } else {
+        o = *reinterpret_cast<const offz_t*>(&s_off[(sb + e) * Z]);
+      }
+#pragma unroll
+      for (int z = 0; z < Z; ++z) {
+        const uint32_t oz = (Z == 1) ? (uint32_t)o[0] : (uint32_t)o[z];
+        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)((oz | dead) + lane_off), 0, 0);
+      }
+    }
+  };
+
+  // one tile: optional prefetch of tile t+2, unpack, MFMA, group epilogue
+  auto step = [&](int t, uint32_t (&Dc)[8][Z], const u32x2_t& mbc, bool prefetch, uint32_t (&Dn)[8][Z],
+                  u32x2_t& mbn) {
+    const int gt = tile0 + t;  // absolute tile
+    const bool first_of_group = (t == t_begin) || (gt % tiles_per_group == 0);
+    const bool last_of_group = (t + 1 == t_end) || ((gt + 1) % tiles_per_group == 0);
+    if (first_of_group) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        Cv[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) C[mt][jj][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    if (prefetch) issue(t + 2, Dn, mbn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int sb = t * 32 + 8 * q;
+    const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[sb]);
+
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile] from LDS
+    u32x4_t A[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
+
+    // Rebuild the code bytes.  With G_z = rot(D_z, 2z) (plane z's digit of
+    // slot j now sits at field 3-z-j of its byte), output dword j is
+    //   V_j = rot(H_j, -2j),  H_j = field-wise merge taking field (3-z-j)&3 from G_z,
+    // and zone 0's sign flip (offset binary) is applied to D_0 up front.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if ((mbc[e >> 2] >> (8 * (e & 3))) & 1u) Dc[e][0] ^= 0xAAAAAAAAu;
+#pragma unroll
+      for (int z = 1; z < Z; ++z) Dc[e][z] = rotr(Dc[e][z], (uint32_t)(2 * z));
+    }
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      const int j = jg * NJ + jj;
+      uint32_t V[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t h = 0;
+#pragma unroll
+        for (int z = 0; z < Z; ++z) {
+          const int f = (3 - z - j) & 3;  // field taken from G_z
+          h |= Dc[e][z] & (0x03030303u << (2 * f));
+        }
+        V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
+      }
+      u32x4_t B[4];
+      BOperand<DT>::build(V, B);
 #pragma unroll
       for (int b = 0; b < 4; ++b)
-        sraw[jj][b] = p.scale[(int64_t)g * p.N + (int64_t)(4 * (jg * NJ + jj) + b) * p.NW + wc];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      Cv[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) C[mt][jj][b] = mfma16x16x32<DT>(A[mt], B[b], C[mt][jj][b]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) Cv[mt] = mfma16x16x32<DT>(A[mt], bv, Cv[mt]);
+
+    if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv), scales from LDS
+      const uint16_t* srow = &s_scale[(gt / tiles_per_group - g_first) * 256 + 64 * jg * NJ + c];
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) C[mt][jj][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-
-    for (; t < t_stop; ++t) {
-      const int k0 = row0 + t * 32;
-      const int rr = t * 32 + 8 * q;
-      const u32x2_t mb = *reinterpret_cast<const u32x2_t*>(&s_bits[rr]);
-      const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[rr]);
-
-      uint32_t D[8][Z];
-      uint32_t init[8];
+        for (int b = 0; b < 4; ++b) {
+          const float sc = to_f32<DT>(srow[(4 * jj + b) * 16]) * post;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t bits = (mb[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-        init[e] = (bits & 1u) ? 0x80808080u : 0u;
-        const uint32_t* rowp = pbase + (int64_t)(k0 + 8 * q + e) * rstride;
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int z = 0; z < Z; ++z) {
-          D[e][z] = (col_ok && ((bits >> z) & 1u)) ? __builtin_nontemporal_load(rowp + (int64_t)z * p.NW) : 0u;
+            for (int e = 0; e < 4; ++e) Y[mt][jj][b][e] = fmaf(sc, C[mt][jj][b][e] + Cv[mt][e], Y[mt][jj][b][e]);
         }
-      }
-
-      u32x4_t A[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(xrow[mt] + k0);
-
-#pragma unroll
-      for (int jj = 0; jj < NJ; ++jj) {
-        const int j = jg * NJ + jj;
-        uint32_t V[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) V[e] = rebuild_dword<Z>(D[e], init[e], j);
-        u32x4_t B[4];
-        BOperand<DT>::build(V, B);
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) C[mt][jj][b] = mfma16x16x32<DT>(A[mt], B[b], C[mt][jj][b]);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) Cv[mt] = mfma16x16x32<DT>(A[mt], bv, Cv[mt]);
     }
+  };
 
-    // group epilogue: y += s[g][n] * 2^-sh * (C + Cv)
-#pragma unroll
-    for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float sc = to_f32<DT>(sraw[jj][b]) * post;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) Y[mt][jj][b][e] = fmaf(sc, C[mt][jj][b][e] + Cv[mt][e], Y[mt][jj][b][e]);
-      }
+  {
+    // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
+    uint32_t DA[8][Z], DB[8][Z], DC[8][Z];
+    u32x2_t mbA, mbB, mbC;
+    issue(t_begin, DA, mbA);
+    issue(t_begin + 1, DB, mbB);
+    int t = t_begin;
+    for (; t + 3 <= t_end; t += 3) {
+      step(t, DA, mbA, true, DC, mbC);
+      step(t + 1, DB, mbB, true, DA, mbA);
+      step(t + 2, DC, mbC, true, DB, mbB);
+    }
+    // at most two tiles left, already loaded into DA and DB
+    if (t < t_end) step(t, DA, mbA, false, DC, mbC);
+    if (t + 1 < t_end) step(t + 1, DB, mbB, false, DC, mbC);
   }
 
-  // ---- phase 3: reduce the K sub-ranges of this block (fixed order)
+  // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...
+  // (the staging area is free now and holds one slot per contributing wave)
   if (KW > 1) {
+    __syncthreads();
     if (kw > 0) {
-      const int slot = (kw - 1) * MT + jg;
+      f32x4_t* slot = s_red + ((kw - 1) * MT + jg) * 16 * 64;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) s_red[(slot * 16 + (mt * NJ + jj) * 4 + b) * 64 + lane] = Y[mt][jj][b];
+          for (int b = 0; b < 4; ++b) slot[((mt * NJ + jj) * 4 + b) * 64 + lane] = Y[mt][jj][b];
     }
     __syncthreads();
     if (kw == 0) {
+#pragma unroll
       for (int k2 = 1; k2 < KW; ++k2) {
-        const int slot = (k2 - 1) * MT + jg;
+        const f32x4_t* slot = s_red + ((k2 - 1) * MT + jg) * 16 * 64;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) Y[mt][jj][b] += s_red[(slot * 16 + (mt * NJ + jj) * 4 + b) * 64 + lane];
+            for (int b = 0; b < 4; ++b) Y[mt][jj][b] += slot[((mt * NJ + jj) * 4 + b) * 64 + lane];
       }
     }
   }
 
   // ---- phase 4: output (direct, or split-K partials + last-block reduction)
   // Output (m, n) of this lane: m = 16*mt + 4*q + e, n = (4*(jg*NJ+jj)+b)*NW + w0 + c.
-  // Loads below use clamped (in-bounds) rows/columns so they carry no branches
-  // and issue back to back; only the stores are predicated.
   auto col_of = [&](int jj, int b) -> int64_t { return (int64_t)(4 * (jg * NJ + jj) + b) * p.NW + wc; };
-  auto store_final = [&](const f32x4_t (&R)[MT][NJ][4]) {
-    uint16_t braw[NJ][4];
-#pragma unroll
-    for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) braw[jj][b] = p.bias != nullptr ? p.bias[col_of(jj, b)] : (uint16_t)0;
-    if (!col_ok) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = 16 * mt + 4 * q + e;
-            if (m < p.M) {
-              uint16_t v = from_f32<DT>(R[mt][jj][b][e]);
-              if (p.bias != nullptr) v = from_f32<DT>(to_f32<DT>(v) + to_f32<DT>(braw[jj][b]));
-              p.y[(int64_t)m * p.N + col_of(jj, b)] = v;
-            }
-          }
-  };
-
   if (p.splits == 1) {
-    if (kw == 0) store_final(Y);
+    if (kw == 0 && col_ok) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int m = 16 * mt + 4 * q + e;
+              if (m < p.M) p.y[(int64_t)m * p.N + col_of(jj, b)] = finish_output<DT>(Y[mt][jj][b][e], p.bias,
+                                                                                  (int)col_of(jj, b));
+            }
+    }
     return;
   }
 
+  // Split-K: partials go out with agent-scope (write-through) stores; once a
+  // thread's stores have completed (vmcnt 0) the block counts itself in.  The
+  // block that arrives last reads every partial with agent-scope loads, sums
+  // them in fixed order 0..splits-1 and writes the output.  Device-coherent
+  // stores and loads need no L2 write-back or invalidate.
   if (kw == 0 && col_ok) {
     float* part = p.partial + (int64_t)split * p.M * p.N;
 #pragma unroll
@@ -278,43 +404,43 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(DecodeParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int m = 16 * mt + 4 * q + e;
-            if (m < p.M) part[(int64_t)m * p.N + col_of(jj, b)] = Y[mt][jj][b][e];
+            if (m < p.M)
+              __hip_atomic_store(&part[(int64_t)m * p.N + col_of(jj, b)], Y[mt][jj][b][e], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
           }
   }
-  __threadfence();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[blockIdx.x], 1u);
+    const unsigned prev = __hip_atomic_fetch_add(&p.counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == (unsigned)(p.splits - 1)) ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  if (kw == 0) {
-    // sum the K ranges in fixed order 0..splits-1 (independent of arrival order)
+  asm volatile("" ::: "memory");
+  const int ncols = 16 * min(16, p.NW - w0);  // valid (tile, column) pairs of this block: 16 per tile
+  for (int o = tid; o < p.M * 256; o += 256) {
+    const int m = o >> 8, col = o & 255;
+    const int r = col >> 4, cc = col & 15;
+    if (cc >= ncols / 16) continue;
+    const int64_t n = (int64_t)r * p.NW + w0 + cc;
+    const float* pp = p.partial + (int64_t)m * p.N + n;
+    const int64_t stride = (int64_t)p.M * p.N;
+    float acc = 0.f;
+    int s2 = 0;
+    for (; s2 + 8 <= p.splits; s2 += 8) {
+      float v[8];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int i = 0; i < 8; ++i)
+        v[i] = __hip_atomic_load(pp + (s2 + i) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-      for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) Y[mt][jj][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int s2 = 0; s2 < p.splits; ++s2) {
-      const float* part = p.partial + (int64_t)s2 * p.M * p.N;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int m = min(16 * mt + 4 * q + e, p.M - 1);
-              Y[mt][jj][b][e] += part[(int64_t)m * p.N + col_of(jj, b)];
-            }
+      for (int i = 0; i < 8; ++i) acc += v[i];
     }
-    store_final(Y);
+    for (; s2 < p.splits; ++s2) acc += __hip_atomic_load(pp + s2 * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    p.y[(int64_t)m * p.N + n] = finish_output<DT>(acc, p.bias, (int)n);
   }
-  if (tid == 0) p.counters[blockIdx.x] = 0u;
+  if (tid == 0) __hip_atomic_store(&p.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // sigma_k = max_m |x[m][k]| over the whole batch (NaN ignored unless all NaN),
@@ -334,7 +460,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   pl.col_blocks = (int)((NW + 15) / 16);
   const int64_t T = K / 32;
   const int kw = 4 / pl.mt;
-  const int64_t tiles_max = kDecodeRowsMax / 32;
+  const int64_t tiles_max = kDecodeRowsPerBlock / pl.mt / 32;
   const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
   const int64_t want = (512 + pl.col_blocks - 1) / pl.col_blocks;
   int64_t max_splits = T / (2 * kw);
