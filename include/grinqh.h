@@ -84,17 +84,18 @@ int grinqh_dequantize(const void* planes_u32, const void* scale, void* out, int6
 int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, int max_bits,
                  const float thresholds[4], uint8_t* zone_bits, int32_t* beta, void* stream);
 
-/* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none).  The
- * first 4096 bytes are counters: zero them once when the workspace is
- * allocated; every call leaves them zero again.  Calls that share a workspace
- * must be ordered (same stream). */
+/* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none): fp32
+ * split-K partial sums and, for union batches of more than 64 rows, the
+ * per-row grading statistic.  No initial contents are required.  Calls that
+ * share a workspace must be ordered (same stream); it must be 256-byte aligned. */
 size_t grinqh_workspace_bytes(int64_t M, int64_t K, int64_t N, int max_bits, int mode);
 
 /* The quantized linear y[M][N] = x[M][K] * W_eff (+ bias), x/scale/bias/y in `dtype`.
  * Replaces torch.ops.grinqh.gemm_or_gemv (grinqh/kernel.py:646-710); N here is
  * 4 * original_n.  thresholds: 4 fp32 values (zero padded like
- * grinqh/grinqh.py:111).  x rows are ldx elements apart (ldx % 8 == 0), y is
- * dense [M][N].  K % 32 == 0, N % 16 == 0, group_size % 32 == 0. */
+ * grinqh/grinqh.py:111).  x rows are ldx elements apart (ldx % 8 == 0, x
+ * 16-byte aligned), y is dense [M][N] (8-byte aligned).  K % 32 == 0,
+ * N % 16 == 0, group_size % 32 == 0. */
 int grinqh_gemm_or_gemv(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
                         const void* planes_u32, const void* scale, const void* bias, void* y,
                         int max_bits, int group_size, const float thresholds[4], int mode,

@@ -41,9 +41,9 @@ def test_version_and_status_strings(lib):
 
 
 def test_workspace_query(lib):
-    # M=1 o_proj shape: split-K partials are needed; counters come first.
+    # M=1 o_proj shape: split-K needs one fp32 [M][N] slab per K range.
     ws = lib.grinqh_workspace_bytes(1, 4096, 4096, 8, 0)
-    assert ws >= 4096 + 4096 * 4 and (ws - 4096) % (4096 * 4) == 0
+    assert ws >= 2 * 4096 * 4 and ws % (4096 * 4) == 0
     assert lib.grinqh_workspace_bytes(0, 4096, 4096, 8, 0) == 0
     # union batches beyond one launch also carry the K-float sigma area
     assert lib.grinqh_workspace_bytes(200, 4096, 4096, 8, 1) >= lib.grinqh_workspace_bytes(200, 4096, 4096, 8, 2)

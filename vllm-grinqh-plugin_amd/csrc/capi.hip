@@ -24,19 +24,19 @@ struct WorkspaceLayout {
   DecodePlan plan;
 };
 
-// [counters | sigma (K floats, union batches split into several launches) | split-K partials]
+// [sigma (K floats, union batches split into several launches) | split-K partials]
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   const int64_t m_launch = M < kDecodeMaxRows ? M : kDecodeMaxRows;
   w.plan = plan_decode(m_launch > 0 ? m_launch : 1, K, N);
-  size_t partial = w.plan.splits > 1 ? w.plan.workspace - kCounterBytes : 0;
+  size_t partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   if (M > kDecodeMaxRows && M % kDecodeMaxRows != 0) {  // the last, shorter launch may split differently
     const DecodePlan tail = plan_decode(M % kDecodeMaxRows, K, N);
-    const size_t tail_partial = tail.splits > 1 ? tail.workspace - kCounterBytes : 0;
+    const size_t tail_partial = tail.splits > 1 ? tail.workspace : 0;
     if (tail_partial > partial) partial = tail_partial;
   }
   const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kDecodeMaxRows;
-  w.sigma_off = kCounterBytes;
+  w.sigma_off = 0;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
   return w;
@@ -50,7 +50,7 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
   if (K > (int64_t)1 << 30 || N > (int64_t)1 << 24 || M > (int64_t)1 << 30) return GRINQH_ERR_INVALID;
   if (M > 0 && (x == nullptr || planes == nullptr || scale == nullptr || y == nullptr)) return GRINQH_ERR_INVALID;
   if (ldx < K || ldx % 8 != 0 || !aligned(x, 16) || !aligned(planes, 4)) return GRINQH_ERR_INVALID;
-  if ((N / 16 + 15) / 16 > kMaxCounters) return GRINQH_ERR_INVALID;
+  if (!aligned(y, 8) || !aligned(scale, 2)) return GRINQH_ERR_INVALID;
   // plane words are addressed with 32-bit byte offsets (bit 31 reserved)
   if (K * (max_bits / 2) * (N / 16) * 4 >= ((int64_t)1 << 31)) return GRINQH_ERR_INVALID;
   return GRINQH_OK;
@@ -83,7 +83,6 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   p.NW = (int)(N / 16);
   p.gs = group_size;
   for (int i = 0; i < 4; ++i) p.thr.t[i] = graded ? thresholds[i] : 0.f;
-  p.counters = reinterpret_cast<unsigned*>(ws);
   p.partial = ws ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
   p.sigma = nullptr;
 

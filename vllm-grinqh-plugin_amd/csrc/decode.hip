@@ -33,8 +33,8 @@
 // in fp32, as grinqh/kernel.py:148-158 applies scales.
 //
 // Split-K partials are reduced deterministically: the 4/MT waves of a block
-// through LDS in fixed order, the K ranges by the last-arriving block (fixed
-// order over ranges), which also applies the output cast and bias.
+// through LDS in fixed order; the K ranges (grid.y) by a second kernel that
+// adds the fp32 partials in range order and applies the output cast and bias.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 
@@ -101,7 +101,6 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   __shared__ __align__(16) uint8_t s_bits[RMAX];   // row -> zone bits
   __shared__ __align__(16) uint16_t s_bv[RMAX];    // row -> correction-column value
   __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
-  __shared__ int s_last;
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(s_pool);
@@ -388,11 +387,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     return;
   }
 
-  // Split-K: partials go out with agent-scope (write-through) stores; once a
-  // thread's stores have completed (vmcnt 0) the block counts itself in.  The
-  // block that arrives last reads every partial with agent-scope loads, sums
-  // them in fixed order 0..splits-1 and writes the output.  Device-coherent
-  // stores and loads need no L2 write-back or invalidate.
+  // Split-K: this K range's partial sums go to partial[split][m][n]; the
+  // reduce kernel that follows on the stream adds the ranges in fixed order.
   if (kw == 0 && col_ok) {
     float* part = p.partial + (int64_t)split * p.M * p.N;
 #pragma unroll
@@ -404,43 +400,47 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int m = 16 * mt + 4 * q + e;
-            if (m < p.M)
-              __hip_atomic_store(&part[(int64_t)m * p.N + col_of(jj, b)], Y[mt][jj][b][e], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+            if (m < p.M) part[(int64_t)m * p.N + col_of(jj, b)] = Y[mt][jj][b][e];
           }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = __hip_atomic_fetch_add(&p.counters[blockIdx.x], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == (unsigned)(p.splits - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  asm volatile("" ::: "memory");
-  const int ncols = 16 * min(16, p.NW - w0);  // valid (tile, column) pairs of this block: 16 per tile
-  for (int o = tid; o < p.M * 256; o += 256) {
-    const int m = o >> 8, col = o & 255;
-    const int r = col >> 4, cc = col & 15;
-    if (cc >= ncols / 16) continue;
-    const int64_t n = (int64_t)r * p.NW + w0 + cc;
-    const float* pp = p.partial + (int64_t)m * p.N + n;
-    const int64_t stride = (int64_t)p.M * p.N;
-    float acc = 0.f;
-    int s2 = 0;
-    for (; s2 + 8 <= p.splits; s2 += 8) {
-      float v[8];
+}
+
+// y[m][n] = cast(sum_{s=0..splits-1} partial[s][m][n]) (+ bias): four
+// consecutive columns per thread, the ranges added in order 0, 1, ... with up
+// to 16 loads in flight.
+template <typename DT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M,
+                                                            int N, const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // index of a 4-column chunk
+  const int64_t total = (int64_t)M * N / 4;
+  if (i >= total) return;
+  const int64_t stride = (int64_t)M * N / 4;
+  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(partial) + i;
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  int s = 0;
+  for (; s + 16 <= splits; s += 16) {
+    f32x4_t v[16];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        v[i] = __hip_atomic_load(pp + (s2 + i) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < 16; ++k) v[k] = __builtin_nontemporal_load(src + (int64_t)(s + k) * stride);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc += v[i];
-    }
-    for (; s2 < p.splits; ++s2) acc += __hip_atomic_load(pp + s2 * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    p.y[(int64_t)m * p.N + n] = finish_output<DT>(acc, p.bias, (int)n);
+    for (int k = 0; k < 16; ++k) acc += v[k];
   }
-  if (tid == 0) __hip_atomic_store(&p.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (s < splits) {
+    f32x4_t v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (s + k < splits) v[k] = __builtin_nontemporal_load(src + (int64_t)(s + k) * stride);
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (s + k < splits) acc += v[k];
+  }
+  const int n = (int)((i * 4) % N);
+  uint16_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = finish_output<DT>(acc[e], bias, n + e);
+  *reinterpret_cast<u32x2_t*>(y + i * 4) = u32x2_t{(uint32_t)o[0] | ((uint32_t)o[1] << 16),
+                                                   (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
 }
 
 // sigma_k = max_m |x[m][k]| over the whole batch (NaN ignored unless all NaN),
@@ -480,7 +480,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   if (splits < 1) splits = 1;
   pl.splits = (int)splits;
   pl.tiles_per_split = (int)tps;
-  pl.workspace = splits > 1 ? kCounterBytes + (size_t)(splits * bytes_per_split) : 0;
+  pl.workspace = splits > 1 ? (size_t)(splits * bytes_per_split) : 0;
   return pl;
 }
 
@@ -521,6 +521,16 @@ int launch_decode(const DecodeParams& p, const DecodePlan& pl, int max_bits, int
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_decode_dt<BF16>(p, pl, Z, dense, st)
                                             : launch_decode_dt<F16>(p, pl, Z, dense, st);
   if (rc != GRINQH_OK) return rc;
+  if (pl.splits > 1) {
+    const int64_t chunks = (int64_t)p.M * p.N / 4;
+    const dim3 grid((unsigned)((chunks + 255) / 256));
+    if (dtype == GRINQH_DTYPE_BF16)
+      hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, dim3(256), 0, st, p.partial, pl.splits, p.M, p.N, p.bias,
+                         p.y);
+    else
+      hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, dim3(256), 0, st, p.partial, pl.splits, p.M, p.N, p.bias,
+                         p.y);
+  }
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

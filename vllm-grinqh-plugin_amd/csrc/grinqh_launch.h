@@ -12,9 +12,6 @@ struct GradeThresholds {
   float t[4];
 };
 
-// Counters live in the first kCounterBytes of the workspace.
-constexpr size_t kCounterBytes = 4096;
-constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(unsigned));
 // Upper bound on the split-K partial-sum area.
 constexpr size_t kMaxPartialBytes = size_t(64) << 20;
 
@@ -30,7 +27,6 @@ struct DecodeParams {
   int splits;           // grid.y: K ranges
   int tiles_per_split;  // 32-row tiles per K range
   float* partial;       // [splits][M][N] fp32 when splits > 1
-  unsigned* counters;   // [grid.x] arrival counters when splits > 1
   const float* sigma;   // optional precomputed union statistic [K] (else computed from x)
 };
 
@@ -39,7 +35,7 @@ struct DecodePlan {
   int splits;
   int tiles_per_split;
   int col_blocks;
-  size_t workspace;  // bytes incl. counters, 0 if splits == 1
+  size_t workspace;  // partial-sum bytes, 0 if splits == 1
 };
 
 DecodePlan plan_decode(int64_t M, int64_t K, int64_t N);

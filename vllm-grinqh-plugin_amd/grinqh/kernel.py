@@ -40,11 +40,10 @@ def batch_grading_mode() -> str:
 
 
 class _Workspaces:
-    """Per (device, stream) scratch for split-K partials and arrival counters.
+    """Per (device, stream) scratch for split-K partial sums.
 
-    Grown on demand with ``torch.zeros`` (counters must start at zero; every
-    call leaves them zero).  Calls on one stream are ordered, so they may share
-    it; different streams get different buffers."""
+    Grown on demand (no initial contents are needed).  Calls on one stream are
+    ordered, so they may share it; different streams get different buffers."""
 
     def __init__(self):
         self._bufs = {}
@@ -62,7 +61,7 @@ class _Workspaces:
                         "GRINQH: workspace must be allocated before graph capture; run the largest "
                         "batch once eagerly first")
                 size = max(nbytes, 1 << 20)
-                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                buf = torch.empty(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
