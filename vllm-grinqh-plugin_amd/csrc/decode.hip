@@ -40,32 +40,33 @@
 
 namespace grinqh {
 
-constexpr int kDecodeRowsPerBlock = 1024;  // rows per block at MT = 1 (x staged in LDS)
+constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged in LDS)
+constexpr int64_t kTargetBlocks = 256;     // MI355X compute units
 
 template <typename DT>
 struct BOperand;
 
-// fp16: B = 1024 + u, built as 0x64 in the high byte and the code byte in the low byte.
+// fp16: B = u as a subnormal, u * 2^-24 (exact: u < 2^10); built with one
+// v_perm per register from the code bytes of two consecutive rows.
 template <>
 struct BOperand<F16> {
-  static constexpr float kBase = 1024.f;
+  static constexpr float kUnit = 16777216.f;  // 2^24: undoes the subnormal scaling
   __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t lo = perm(V[2 * p + 1], V[2 * p], 0x05010400u);  // a0 b0 a1 b1
-      const uint32_t hi = perm(V[2 * p + 1], V[2 * p], 0x07030602u);  // a2 b2 a3 b3
-      B[0][p] = perm(0x64646464u, lo, 0x04010400u);
-      B[1][p] = perm(0x64646464u, lo, 0x04030402u);
-      B[2][p] = perm(0x64646464u, hi, 0x04010400u);
-      B[3][p] = perm(0x64646464u, hi, 0x04030402u);
-    }
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta)
+        B[beta][p] = perm(V[2 * p + 1], V[2 * p], 0x0C040C00u + (uint32_t)beta * 0x00010001u);
+  }
+  __device__ __forceinline__ static uint16_t correction(int v) {  // v * 2^-24, |v| < 1024
+    return v >= 0 ? (uint16_t)v : (uint16_t)(0x8000u | (uint32_t)(-v));
   }
 };
 
 // bf16: B = u (0..255 has at most 8 significant bits, exact in bf16).
 template <>
 struct BOperand<BF16> {
-  static constexpr float kBase = 0.f;
+  static constexpr float kUnit = 1.f;
   __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -77,6 +78,7 @@ struct BOperand<BF16> {
       }
     }
   }
+  __device__ __forceinline__ static uint16_t correction(int v) { return from_f32<BF16>((float)v); }
 };
 
 template <typename DT, int MT, int Z, bool DENSE>
@@ -98,7 +100,6 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 
   // staging area: x rows and (row, plane) offsets; reused for the in-block reduction
   __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
-  __shared__ __align__(16) uint8_t s_bits[RMAX];   // row -> zone bits
   __shared__ __align__(16) uint16_t s_bv[RMAX];    // row -> correction-column value
   __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
@@ -134,7 +135,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
       const int m = mb + k * (256 / CPR);
-      const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
+      const uint32_t off =
+          (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
       xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
     const bool vec_scales = (p.NW % 8) == 0;
@@ -169,7 +171,11 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // ---- phase 1b: grade each row: zone bits, correction-column value, plane offsets
+  // ---- phase 1b: grade each row: correction-column value and plane offsets
+  // The code bytes are consumed in offset binary: zone 0's digits are flipped
+  // for every row (also rows whose zone 0 is inactive and reads as zero), so
+  // the byte is u = int8(U & mask) + 128 and the column value removes the 128:
+  //   w_eff * 2^sh = u + (beta * 2^sh - 128).
   for (int rr = tid; rr < R; rr += 256) {
     uint32_t bits;
     if (DENSE) {
@@ -184,10 +190,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       }
       bits = zone_bits<Z>(s, p.thr.t);
     }
-    s_bits[rr] = (uint8_t)bits;
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
-    const float off = BOperand<DT>::kBase + ((bits & 1u) ? 128.f : 0.f);
-    s_bv[rr] = from_f32<DT>((float)(beta * (1 << SH)) - off);
+    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - 128);
     const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
 #pragma unroll
     for (int z = 0; z < Z; ++z)
@@ -210,25 +214,28 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   // outputs are never stored), so every address below is in bounds.
   const bool col_ok = (w0 + c) < p.NW;
   const int wc = col_ok ? (w0 + c) : (p.NW - 1);
-  const float post = 1.0f / (float)(1 << SH);
+  const float post = BOperand<DT>::kUnit / (float)(1 << SH);
   const int t_begin = (nt * kw) / KW, t_end = (nt * (kw + 1)) / KW;
   const int tiles_per_group = p.gs >> 5;
 
   // Plane words come from raw buffer loads: a (row, plane) a lane does not
   // need has offset bit 31 set, past the buffer end, which returns 0 without a
-  // memory access.  The main loop issues every load unconditionally (tiles past
-  // the end of the range are entirely out of bounds), so wait counts stay
+  // memory access.  The main loop issues every load unconditionally; tiles past
+  // the end of the wave's range go through a descriptor of size 0, so every
+  // one of their loads returns 0 without touching memory.  Wait counts stay
   // static and two prefetched tiles remain in flight.
-  const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(p.planes), (short)0, (int)((uint64_t)p.K * (uint32_t)(Z * p.NW) * 4u), 0x00020000);
+  const int plane_bytes = (int)((uint64_t)p.K * (uint32_t)(Z * p.NW) * 4u);
+  const __amdgpu_buffer_rsrc_t prsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.planes), (short)0, plane_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prsrc_none =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.planes), (short)0, 0, 0x00020000);
   const uint32_t lane_off = (uint32_t)wc * 4u;
 
   typedef uint32_t offz_t __attribute__((ext_vector_type(Z)));
-  auto issue = [&](int t, uint32_t (&D)[8][Z], u32x2_t& mb) {
+  auto issue = [&](int t, uint32_t (&D)[8][Z]) {
     const bool live = t < t_end;
+    const __amdgpu_buffer_rsrc_t rs = live ? prsrc : prsrc_none;
     const int sb = (live ? t : t_begin) * 32 + 8 * q;
-    mb = *reinterpret_cast<const u32x2_t*>(&s_bits[sb]);
-    const uint32_t dead = live ? 0u : 0x80000000u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       offz_t o;
@@ -240,28 +247,17 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int z = 0; z < Z; ++z) {
         const uint32_t oz = (Z == 1) ? (uint32_t)o[0] : (uint32_t)o[z];
-        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)((oz | dead) + lane_off), 0, 0);
+        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
       }
     }
   };
 
   // one tile: optional prefetch of tile t+2, unpack, MFMA, group epilogue
-  auto step = [&](int t, uint32_t (&Dc)[8][Z], const u32x2_t& mbc, bool prefetch, uint32_t (&Dn)[8][Z],
-                  u32x2_t& mbn) {
+  auto step = [&](int t, uint32_t (&Dc)[8][Z], bool prefetch, uint32_t (&Dn)[8][Z]) {
     const int gt = tile0 + t;  // absolute tile
     const bool first_of_group = (t == t_begin) || (gt % tiles_per_group == 0);
     const bool last_of_group = (t + 1 == t_end) || ((gt + 1) % tiles_per_group == 0);
-    if (first_of_group) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        Cv[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-          for (int b = 0; b < 4; ++b) C[mt][jj][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      }
-    }
-    if (prefetch) issue(t + 2, Dn, mbn);
+    if (prefetch) issue(t + 2, Dn);
     __builtin_amdgcn_sched_barrier(0);
 
     const int sb = t * 32 + 8 * q;
@@ -272,13 +268,15 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
 
-    // Rebuild the code bytes.  With G_z = rot(D_z, 2z) (plane z's digit of
-    // slot j now sits at field 3-z-j of its byte), output dword j is
+    // Rebuild the code bytes.  Plane z's digit of slot j sits in field 3-j of
+    // each byte (bits 8*beta + 6 - 2j); after G_z = rot(D_z, 2z) it sits in
+    // field (3-z-j)&3, so output dword j is
     //   V_j = rot(H_j, -2j),  H_j = field-wise merge taking field (3-z-j)&3 from G_z,
-    // and zone 0's sign flip (offset binary) is applied to D_0 up front.
+    // a bit-field insert per plane.  Zone 0's top digit bit is flipped first
+    // (offset binary).
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      if ((mbc[e >> 2] >> (8 * (e & 3))) & 1u) Dc[e][0] ^= 0xAAAAAAAAu;
+      Dc[e][0] ^= 0xAAAAAAAAu;
 #pragma unroll
       for (int z = 1; z < Z; ++z) Dc[e][z] = rotr(Dc[e][z], (uint32_t)(2 * z));
     }
@@ -288,23 +286,32 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       uint32_t V[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        uint32_t h = 0;
+        // the planes' fields are disjoint: with all four planes the last one
+        // fills the remaining field, otherwise the fields no plane owns are zero
+        uint32_t h = (Z == 4) ? Dc[e][3] : (Dc[e][0] & (0x03030303u << (2 * ((3 - j) & 3))));
 #pragma unroll
-        for (int z = 0; z < Z; ++z) {
-          const int f = (3 - z - j) & 3;  // field taken from G_z
-          h |= Dc[e][z] & (0x03030303u << (2 * f));
-        }
+        for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
+          h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), Dc[e][z], h);
         V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
       }
       u32x4_t B[4];
       BOperand<DT>::build(V, B);
+      // the first tile of a scale group starts its sums from zero
+      if (first_of_group) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) C[mt][jj][b] = mfma16x16x32<DT>(A[mt], B[b], C[mt][jj][b]);
+          for (int mt = 0; mt < MT; ++mt) C[mt][jj][b] = mfma16x16x32<DT>(A[mt], B[b], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) C[mt][jj][b] = mfma16x16x32<DT>(A[mt], B[b], C[mt][jj][b]);
+      }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) Cv[mt] = mfma16x16x32<DT>(A[mt], bv, Cv[mt]);
+    for (int mt = 0; mt < MT; ++mt)
+      Cv[mt] = mfma16x16x32<DT>(A[mt], bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv[mt]);
 
     if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv), scales from LDS
       const uint16_t* srow = &s_scale[(gt / tiles_per_group - g_first) * 256 + 64 * jg * NJ + c];
@@ -324,18 +331,17 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   {
     // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
     uint32_t DA[8][Z], DB[8][Z], DC[8][Z];
-    u32x2_t mbA, mbB, mbC;
-    issue(t_begin, DA, mbA);
-    issue(t_begin + 1, DB, mbB);
+    issue(t_begin, DA);
+    issue(t_begin + 1, DB);
     int t = t_begin;
     for (; t + 3 <= t_end; t += 3) {
-      step(t, DA, mbA, true, DC, mbC);
-      step(t + 1, DB, mbB, true, DA, mbA);
-      step(t + 2, DC, mbC, true, DB, mbB);
+      step(t, DA, true, DC);
+      step(t + 1, DB, true, DA);
+      step(t + 2, DC, true, DB);
     }
     // at most two tiles left, already loaded into DA and DB
-    if (t < t_end) step(t, DA, mbA, false, DC, mbC);
-    if (t + 1 < t_end) step(t + 1, DB, mbB, false, DC, mbC);
+    if (t < t_end) step(t, DA, false, DC);
+    if (t + 1 < t_end) step(t + 1, DB, false, DC);
   }
 
   // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...
@@ -462,7 +468,9 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   const int kw = 4 / pl.mt;
   const int64_t tiles_max = kDecodeRowsPerBlock / pl.mt / 32;
   const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
-  const int64_t want = (512 + pl.col_blocks - 1) / pl.col_blocks;
+  // one block per CU, all blocks resident at once: the per-block set-up
+  // (staging, grading) is paid once per CU rather than once per round
+  const int64_t want = kTargetBlocks / pl.col_blocks > 0 ? kTargetBlocks / pl.col_blocks : 1;
   int64_t max_splits = T / (2 * kw);
   if (max_splits < 1) max_splits = 1;
   int64_t splits = want < max_splits ? want : max_splits;

@@ -137,20 +137,13 @@ __device__ __forceinline__ int midpoint_bias(uint32_t bits) {
 
 // ---------------------------------------------------------------- unpack
 
-// Rebuild the masked code bytes V_j (one byte per column tile 4j+beta) of one
-// row from its plane words D[z]; planes that are inactive for the row must be
-// passed as 0.  The result is (U & mask) with U = code << (8-b), XOR 0x80 in
-// every byte when zone 0 is active, i.e. offset-binary int8(U & mask) + 128.
-// Bits 8b+6-2j of D[z] move to 8b+6-2z: a rotation by 2(z-j) mod 32.
-template <int Z>
-__device__ __forceinline__ uint32_t rebuild_dword(const uint32_t (&D)[Z], uint32_t init, int j) {
-  uint32_t v = init;
-#pragma unroll
-  for (int z = 0; z < Z; ++z) {
-    const uint32_t m = 0xC0C0C0C0u >> (2 * z);
-    v ^= rotr(D[z], (uint32_t)(2 * (z - j)) & 31u) & m;
-  }
-  return v;
+// Bit-field insert (v_bfi_b32): bits of `a` where `m` is set, bits of `b` elsewhere.
+// Written as one instruction: left to itself the compiler splits chains of
+// these with constant masks into and/or sequences of twice the length.
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
+  return r;
 }
 
 }  // namespace grinqh
