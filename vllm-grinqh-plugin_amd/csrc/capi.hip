@@ -24,14 +24,20 @@ struct WorkspaceLayout {
   DecodePlan plan;
 };
 
+// Plan of one launch of mc rows: the GEMV kernel up to kGemvMaxRows rows, the
+// decode kernel above.  group_size 32 gives the largest GEMV workspace.
+DecodePlan plan_launch(int64_t mc, int64_t K, int64_t N, int64_t group_size) {
+  return mc <= kGemvMaxRows ? plan_gemv(mc, K, N, group_size) : plan_decode(mc, K, N);
+}
+
 // [sigma (K floats, union batches split into several launches) | split-K partials]
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   const int64_t m_launch = M < kDecodeMaxRows ? M : kDecodeMaxRows;
-  w.plan = plan_decode(m_launch > 0 ? m_launch : 1, K, N);
+  w.plan = plan_launch(m_launch > 0 ? m_launch : 1, K, N, 32);
   size_t partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   if (M > kDecodeMaxRows && M % kDecodeMaxRows != 0) {  // the last, shorter launch may split differently
-    const DecodePlan tail = plan_decode(M % kDecodeMaxRows, K, N);
+    const DecodePlan tail = plan_launch(M % kDecodeMaxRows, K, N, 32);
     const size_t tail_partial = tail.splits > 1 ? tail.workspace : 0;
     if (tail_partial > partial) partial = tail_partial;
   }
@@ -96,13 +102,14 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   }
   for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
-    const DecodePlan plan = plan_decode(mc, K, N);
+    const DecodePlan plan = plan_launch(mc, K, N, group_size);
     p.x = xs + m0 * ldx;
     p.y = ys + m0 * N;
     p.M = (int)mc;
     p.splits = plan.splits;
     p.tiles_per_split = plan.tiles_per_split;
-    rc = launch_decode(p, plan, max_bits, dtype, !graded, st);
+    rc = mc <= kGemvMaxRows ? launch_gemv(p, plan, max_bits, dtype, !graded, st)
+                            : launch_decode(p, plan, max_bits, dtype, !graded, st);
     if (rc != GRINQH_OK) return rc;
   }
   return GRINQH_OK;

@@ -41,45 +41,6 @@
 namespace grinqh {
 
 constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged in LDS)
-constexpr int64_t kTargetBlocks = 256;     // MI355X compute units
-
-template <typename DT>
-struct BOperand;
-
-// fp16: B = u as a subnormal, u * 2^-24 (exact: u < 2^10); built with one
-// v_perm per register from the code bytes of two consecutive rows.
-template <>
-struct BOperand<F16> {
-  static constexpr float kUnit = 16777216.f;  // 2^24: undoes the subnormal scaling
-  __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int beta = 0; beta < 4; ++beta)
-        B[beta][p] = perm(V[2 * p + 1], V[2 * p], 0x0C040C00u + (uint32_t)beta * 0x00010001u);
-  }
-  __device__ __forceinline__ static uint16_t correction(int v) {  // v * 2^-24, |v| < 1024
-    return v >= 0 ? (uint16_t)v : (uint16_t)(0x8000u | (uint32_t)(-v));
-  }
-};
-
-// bf16: B = u (0..255 has at most 8 significant bits, exact in bf16).
-template <>
-struct BOperand<BF16> {
-  static constexpr float kUnit = 1.f;
-  __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-#pragma unroll
-      for (int beta = 0; beta < 4; ++beta) {
-        const float a = (float)((V[2 * p] >> (8 * beta)) & 0xFFu);
-        const float b = (float)((V[2 * p + 1] >> (8 * beta)) & 0xFFu);
-        B[beta][p] = perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
-      }
-    }
-  }
-  __device__ __forceinline__ static uint16_t correction(int v) { return from_f32<BF16>((float)v); }
-};
 
 template <typename DT, int MT, int Z, bool DENSE>
 __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
@@ -268,32 +229,13 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
 
-    // Rebuild the code bytes.  Plane z's digit of slot j sits in field 3-j of
-    // each byte (bits 8*beta + 6 - 2j); after G_z = rot(D_z, 2z) it sits in
-    // field (3-z-j)&3, so output dword j is
-    //   V_j = rot(H_j, -2j),  H_j = field-wise merge taking field (3-z-j)&3 from G_z,
-    // a bit-field insert per plane.  Zone 0's top digit bit is flipped first
-    // (offset binary).
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      Dc[e][0] ^= 0xAAAAAAAAu;
-#pragma unroll
-      for (int z = 1; z < Z; ++z) Dc[e][z] = rotr(Dc[e][z], (uint32_t)(2 * z));
-    }
+    // Rebuild the code bytes (offset binary) and turn them into B operands.
+    prepare_planes<Z>(Dc);
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
       const int j = jg * NJ + jj;
       uint32_t V[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // the planes' fields are disjoint: with all four planes the last one
-        // fills the remaining field, otherwise the fields no plane owns are zero
-        uint32_t h = (Z == 4) ? Dc[e][3] : (Dc[e][0] & (0x03030303u << (2 * ((3 - j) & 3))));
-#pragma unroll
-        for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
-          h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), Dc[e][z], h);
-        V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
-      }
+      code_dwords<Z>(Dc, j, V);
       u32x4_t B[4];
       BOperand<DT>::build(V, B);
       // the first tile of a scale group starts its sums from zero
@@ -529,16 +471,17 @@ int launch_decode(const DecodeParams& p, const DecodePlan& pl, int max_bits, int
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_decode_dt<BF16>(p, pl, Z, dense, st)
                                             : launch_decode_dt<F16>(p, pl, Z, dense, st);
   if (rc != GRINQH_OK) return rc;
-  if (pl.splits > 1) {
-    const int64_t chunks = (int64_t)p.M * p.N / 4;
-    const dim3 grid((unsigned)((chunks + 255) / 256));
-    if (dtype == GRINQH_DTYPE_BF16)
-      hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, dim3(256), 0, st, p.partial, pl.splits, p.M, p.N, p.bias,
-                         p.y);
-    else
-      hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, dim3(256), 0, st, p.partial, pl.splits, p.M, p.N, p.bias,
-                         p.y);
-  }
+  if (pl.splits > 1) return launch_splitk_reduce(p, pl.splits, dtype, st);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
+}
+
+int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream_t st) {
+  const int64_t chunks = (int64_t)p.M * p.N / 4;
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  if (dtype == GRINQH_DTYPE_BF16)
+    hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, dim3(256), 0, st, p.partial, splits, p.M, p.N, p.bias, p.y);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, dim3(256), 0, st, p.partial, splits, p.M, p.N, p.bias, p.y);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

@@ -1,0 +1,350 @@
+// GEMV-regime GRINQH product (M <= 4 per launch): graded or dense
+// y = x * W_eff on v_mfma_f32_16x16x32_{f16,bf16}, HBM-bound.
+//
+// Replaces the reference's Triton GEMV grinqh_gemv_uint32_packed
+// (grinqh/kernel.py:39-167, one row), the batch-union GEMV
+// grinqh_gemv_uint32_packed_batch_union (:170-360) for batches of up to four
+// rows, and the dense branch of grinqh_gemm_or_gemv for such batches
+// (:663-680, semantics of :561-587).
+//
+// Each lane owns one plane-word column w = w0 + lane (16 logical columns,
+// one per column tile 4j+beta), so every buffer load of a wave reads one
+// 256-byte run of a (row, plane) line, and a (row, plane) the grading skips is
+// skipped by the whole wave.  The MFMA is used block-diagonally: lane (c, q)
+// supplies B = the 8 rows of the tile for its own column w, and A holds x
+// rows 0..3 only in the q-th 4x8 block of the 16x32 A tile:
+//   A[m][8q' + e] = x[m & 3][row e]  if m >> 2 == q'  else 0,
+// so output rows 4q..4q+3 of column c are y[0..3] of word column 16q + c,
+// exactly the lane that holds them.
+//
+// Work decomposition
+//   grid.x = 64 word columns (1024 logical columns), grid.y = K range
+//   4 waves = 4 consecutive sub-ranges of the K range (8-row tiles), reduced
+//   through LDS in fixed order; K ranges are reduced by the split-K kernel.
+#include "grinqh_common.h"
+#include "grinqh_launch.h"
+
+namespace grinqh {
+
+constexpr int kGemvRowsPerBlock = 1024;   // rows of x staged per block
+constexpr int kGemvScaleGroups = 9;       // scale groups staged per block
+// One row (MR = 1) fits two resident blocks per CU (256 registers per lane);
+// up to four rows (MR = 4) keep one block per CU.
+constexpr int gemv_blocks_per_cu(int mr) { return mr == 1 ? 2 : 1; }
+
+template <typename DT, int MR, int Z, bool DENSE>
+__global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(DecodeParams p) {
+  constexpr int SH = 8 - 2 * Z;
+  constexpr int RMAX = kGemvRowsPerBlock;
+  constexpr int XS = RMAX + 8;                 // halves per staged x row
+  constexpr int X_BYTES = 5 * XS * 2;          // x rows 0..3, row 4 all zero
+  constexpr int OFF_BYTES = RMAX * Z * 4;
+  constexpr int RED_BYTES = 3 * 16 * MR * 64 * 4;  // partial sums of waves 1..3
+  constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_BYTES ? (X_BYTES + OFF_BYTES) : RED_BYTES;
+  constexpr int SCG = kGemvScaleGroups;
+  constexpr int CPR = RMAX / 8;                // 16-byte chunks per staged x row
+  constexpr int XPT = 4 * CPR / 256;
+  constexpr int SCH = SCG * 16 * 8;            // 16-byte scale chunks (group, tile, 8 columns)
+  constexpr int SPT = (SCH + 255) / 256;
+
+  __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
+  __shared__ __align__(16) uint16_t s_bv[RMAX];               // row -> correction-column value
+  __shared__ __align__(16) uint16_t s_scale[SCG * 16 * 64];   // (group, tile, word column) scales
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
+  uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
+  float* s_red = reinterpret_cast<float*>(s_pool);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, q = lane >> 4;
+  const int w0 = blockIdx.x * 64;
+  const int split = blockIdx.y;
+  const int tile0 = split * p.tiles_per_split;
+  const int tile1 = min(tile0 + p.tiles_per_split, p.K >> 5);
+  const int R = (tile1 - tile0) * 32;
+  const int row0 = tile0 * 32;
+  const int g_first = row0 / p.gs;
+  const int n_groups = (row0 + R - 1) / p.gs - g_first + 1;
+  // lanes past the last word column read the last valid one (never stored)
+  const bool col_ok = (w0 + lane) < p.NW;
+  const int wc = col_ok ? (w0 + lane) : (p.NW - 1);
+
+  // ---- phase 1a: stage x rows 0..3 of [row0, row0 + R) and the scales; loads first, then stores.
+  // Out-of-range offsets read 0: rows m >= M stage as zeros.
+  {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
+    const uint32_t sbytes = (uint32_t)((uint64_t)((p.K + p.gs - 1) / p.gs) * p.N * 2u);
+    const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.scale), (short)0, (int)sbytes, 0x00020000);
+    u32x4_t xv[XPT];
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int h = tid + 256 * k, m = h / CPR, u = h % CPR;
+      const uint32_t off =
+          (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
+      xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+    }
+    const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
+    u32x4_t sv[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + 256 * k;
+      const int gl = h >> 7, r = (h >> 3) & 15, h8 = h & 7;
+      const uint32_t off =
+          (h < SCH && gl < n_groups && vec_scales)
+              ? (uint32_t)(((int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + w0 + 8 * h8) * 2)
+              : 0x80000000u;
+      sv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(sr, (int)off, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int h = tid + 256 * k, m = h / CPR, u = h % CPR;
+      *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
+    }
+    if (tid < CPR) *reinterpret_cast<u32x4_t*>(&s_x[4 * XS + 8 * tid]) = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + 256 * k;
+      if (h < SCH) *reinterpret_cast<u32x4_t*>(&s_scale[h * 8]) = sv[k];
+    }
+    if (!vec_scales) {  // element-wise staging
+      for (int idx = tid; idx < n_groups * 1024; idx += 256) {
+        const int gl = idx >> 10, r = (idx >> 6) & 15;
+        const int wcol = min(w0 + (idx & 63), p.NW - 1);
+        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + wcol];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 1b: grade each row: correction-column value and plane offsets (the
+  // code bytes are consumed in offset binary, w_eff * 2^sh = u + beta * 2^sh - 128)
+  for (int rr = tid; rr < R; rr += 256) {
+    uint32_t bits;
+    if (DENSE) {
+      bits = (1u << Z) - 1u;
+    } else {
+      float s;
+      if (p.sigma != nullptr) {  // statistic of a whole batch split into several launches
+        s = p.sigma[row0 + rr];
+      } else {
+        s = fabsf(to_f32<DT>(s_x[rr]));
+        for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
+      }
+      bits = zone_bits<Z>(s, p.thr.t);
+    }
+    const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
+    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - 128);
+    const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
+#pragma unroll
+    for (int z = 0; z < Z; ++z)
+      s_off[rr * Z + z] = ((bits >> z) & 1u) ? row_bytes + (uint32_t)z * (uint32_t)p.NW * 4u : 0x80000000u;
+  }
+  __syncthreads();
+
+  // ---- phase 2: this wave's 8-row tiles
+  f32x4_t C[4][4];
+  f32x4_t Cv;
+  float Y[4][4][MR];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int i = 0; i < MR; ++i) Y[j][b][i] = 0.f;
+
+  const float post = BOperand<DT>::kUnit / (float)(1 << SH);
+  const int n8 = R >> 3;
+  const int t_begin = (n8 * wave) >> 2, t_end = (n8 * (wave + 1)) >> 2;
+  // A operand rows: lane (c, q) carries x row c & 3 when c >> 2 == q, else the zero row
+  const uint16_t* a_row = s_x + (((c >> 2) == q) ? (c & 3) : 4) * XS;
+
+  // Raw buffer loads; a (row, plane) the grading skips has offset bit 31 set
+  // (past the end: reads 0, no memory access).  Tiles past the end of the
+  // wave's range use a descriptor of size 0.  Every load is issued, so wait
+  // counts are static with two tiles in flight.
+  const int plane_bytes = (int)((uint64_t)p.K * (uint32_t)(Z * p.NW) * 4u);
+  const __amdgpu_buffer_rsrc_t prsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.planes), (short)0, plane_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t prsrc_none =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(p.planes), (short)0, 0, 0x00020000);
+  const uint32_t lane_off = (uint32_t)wc * 4u;
+
+  typedef uint32_t offz_t __attribute__((ext_vector_type(Z)));
+  auto issue = [&](int t, uint32_t (&D)[8][Z]) {
+    const bool live = t < t_end;
+    const __amdgpu_buffer_rsrc_t rs = live ? prsrc : prsrc_none;
+    const int sb = (live ? t : t_begin) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      offz_t o;
+      if constexpr (Z == 1) {
+        o = s_off[sb + e];
+      } else {
+        o = *reinterpret_cast<const offz_t*>(&s_off[(sb + e) * Z]);
+      }
+#pragma unroll
+      for (int z = 0; z < Z; ++z) {
+        const uint32_t oz = (Z == 1) ? (uint32_t)o[0] : (uint32_t)o[z];
+        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
+      }
+    }
+  };
+
+  auto step = [&](int t, uint32_t (&Dc)[8][Z], bool prefetch, uint32_t (&Dn)[8][Z]) {
+    const int rowa = row0 + 8 * t;
+    const bool first_of_group = (t == t_begin) || (rowa % p.gs == 0);
+    const bool last_of_group = (t + 1 == t_end) || ((rowa + 8) % p.gs == 0);
+    if (prefetch) issue(t + 2, Dn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const u32x4_t A = *reinterpret_cast<const u32x4_t*>(a_row + 8 * t);
+    const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[8 * t]);
+    prepare_planes<Z>(Dc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t V[8];
+      code_dwords<Z>(Dc, j, V);
+      u32x4_t B[4];
+      BOperand<DT>::build(V, B);
+      if (first_of_group) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) C[j][b] = mfma16x16x32<DT>(A, B[b], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) C[j][b] = mfma16x16x32<DT>(A, B[b], C[j][b]);
+      }
+    }
+    Cv = mfma16x16x32<DT>(A, bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv);
+
+    if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv)
+      const uint16_t* srow = &s_scale[(rowa / p.gs - g_first) * 1024 + lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const float sc = to_f32<DT>(srow[(4 * j + b) * 64]) * post;
+#pragma unroll
+          for (int i = 0; i < MR; ++i) Y[j][b][i] = fmaf(sc, C[j][b][i] + Cv[i], Y[j][b][i]);
+        }
+    }
+  };
+
+  {
+    uint32_t DA[8][Z], DB[8][Z], DC[8][Z];
+    issue(t_begin, DA);
+    issue(t_begin + 1, DB);
+    int t = t_begin;
+    for (; t + 3 <= t_end; t += 3) {
+      step(t, DA, true, DC);
+      step(t + 1, DB, true, DA);
+      step(t + 2, DC, true, DB);
+    }
+    if (t < t_end) step(t, DA, false, DC);
+    if (t + 1 < t_end) step(t + 1, DB, false, DC);
+  }
+
+  // ---- phase 3: add the waves' sub-ranges in order 0, 1, 2, 3
+  __syncthreads();
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int i = 0; i < MR; ++i) s_red[((wave - 1) * 16 * MR + (4 * j + b) * MR + i) * 64 + lane] = Y[j][b][i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int i = 0; i < MR; ++i) Y[j][b][i] += s_red[(k * 16 * MR + (4 * j + b) * MR + i) * 64 + lane];
+
+  // ---- phase 4: output column n = (4j + b) * NW + w of rows m < M
+  if (!col_ok) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int64_t n = (int64_t)(4 * j + b) * p.NW + wc;
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        if (i >= p.M) break;
+        if (p.splits == 1)
+          p.y[(int64_t)i * p.N + n] = finish_output<DT>(Y[j][b][i], p.bias, (int)n);
+        else
+          p.partial[((int64_t)split * p.M + i) * p.N + n] = Y[j][b][i];
+      }
+    }
+}
+
+// The plan sizes K ranges for a group size of 32 (the largest split count);
+// larger groups give at most as many ranges, so the workspace bound holds.
+DecodePlan plan_gemv(int64_t M, int64_t K, int64_t N, int64_t group_size) {
+  DecodePlan pl{};
+  pl.mt = 1;
+  const int64_t NW = N / 16;
+  pl.col_blocks = (int)((NW + 63) / 64);
+  const int64_t T = K / 32;
+  int64_t rows_cap = (int64_t)(kGemvScaleGroups - 1) * group_size;
+  if (rows_cap > kGemvRowsPerBlock) rows_cap = kGemvRowsPerBlock;
+  const int64_t tiles_max = rows_cap / 32 > 0 ? rows_cap / 32 : 1;
+  const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
+  const int64_t target = kTargetBlocks * gemv_blocks_per_cu(M == 1 ? 1 : 4);
+  const int64_t want = target / pl.col_blocks > 0 ? target / pl.col_blocks : 1;
+  int64_t max_splits = T / 2;  // at least two 8-row tiles per wave
+  if (max_splits < 1) max_splits = 1;
+  int64_t splits = want < max_splits ? want : max_splits;
+  if (splits < min_splits) splits = min_splits;
+  int64_t tps = (T + splits - 1) / splits;
+  if (tps < 1) tps = 1;
+  splits = (T + tps - 1) / tps;
+  pl.splits = (int)splits;
+  pl.tiles_per_split = (int)tps;
+  pl.workspace = splits > 1 ? (size_t)(splits * M * N * (int64_t)sizeof(float)) : 0;
+  return pl;
+}
+
+template <typename DT, int MR, int Z>
+static void launch_gemv_t(const DecodeParams& p, const DecodePlan& pl, bool dense, hipStream_t st) {
+  const dim3 grid(pl.col_blocks, pl.splits);
+  if (dense)
+    hipLaunchKernelGGL((gemv_kernel<DT, MR, Z, true>), grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemv_kernel<DT, MR, Z, false>), grid, dim3(256), 0, st, p);
+}
+
+template <typename DT, int MR>
+static int launch_gemv_mr(const DecodeParams& p, const DecodePlan& pl, int Z, bool dense, hipStream_t st) {
+  switch (Z) {
+    case 1: launch_gemv_t<DT, MR, 1>(p, pl, dense, st); break;
+    case 2: launch_gemv_t<DT, MR, 2>(p, pl, dense, st); break;
+    case 3: launch_gemv_t<DT, MR, 3>(p, pl, dense, st); break;
+    case 4: launch_gemv_t<DT, MR, 4>(p, pl, dense, st); break;
+    default: return GRINQH_ERR_INVALID;
+  }
+  return GRINQH_OK;
+}
+
+template <typename DT>
+static int launch_gemv_dt(const DecodeParams& p, const DecodePlan& pl, int Z, bool dense, hipStream_t st) {
+  return p.M == 1 ? launch_gemv_mr<DT, 1>(p, pl, Z, dense, st) : launch_gemv_mr<DT, 4>(p, pl, Z, dense, st);
+}
+
+int launch_gemv(const DecodeParams& p, const DecodePlan& pl, int max_bits, int dtype, bool dense, hipStream_t st) {
+  if (p.M < 1 || p.M > kGemvMaxRows) return GRINQH_ERR_INVALID;
+  const int Z = max_bits / 2;
+  const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_gemv_dt<BF16>(p, pl, Z, dense, st)
+                                            : launch_gemv_dt<F16>(p, pl, Z, dense, st);
+  if (rc != GRINQH_OK) return rc;
+  if (pl.splits > 1) return launch_splitk_reduce(p, pl.splits, dtype, st);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
+}
+
+}  // namespace grinqh

@@ -146,4 +146,78 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
   return r;
 }
 
+// Code-byte rebuild for 8 rows of plane words D[e][z] (one word per plane).
+// Plane z's digit of slot j sits in field 3-j of each byte (bits 8*beta+6-2j).
+// prepare_planes flips zone 0's top digit bit (offset binary: the byte becomes
+// int8(U & mask) + 128, also for rows whose zone 0 was not loaded) and rotates
+// G_z = rot(D_z, 2z), which moves slot j's digit to field (3-z-j)&3; then
+// code_dwords merges field (3-z-j)&3 of every G_z (the fields are disjoint)
+// and rotates back: V_j = rot(H_j, -2j) holds the code bytes of column tiles
+// 4j+beta, digit z in field 3-z.
+template <int Z>
+__device__ __forceinline__ void prepare_planes(uint32_t (&D)[8][Z]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    D[e][0] ^= 0xAAAAAAAAu;
+#pragma unroll
+    for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
+  }
+}
+template <int Z>
+__device__ __forceinline__ void code_dwords(const uint32_t (&G)[8][Z], int j, uint32_t (&V)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // with all four planes the last one fills the remaining field, otherwise
+    // the fields no plane owns are zero
+    uint32_t h = (Z == 4) ? G[e][3] : (G[e][0] & (0x03030303u << (2 * ((3 - j) & 3))));
+#pragma unroll
+    for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
+      h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), G[e][z], h);
+    V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
+  }
+}
+
+// ---------------------------------------------------------------- MFMA B operand
+
+// B registers of v_mfma_f32_16x16x32_{f16,bf16} from rebuilt code bytes: V[e]
+// holds the offset-binary code bytes of row e (byte beta = column tile
+// 4j+beta); B[beta][p] holds rows 2p, 2p+1 of column tile beta.
+template <typename DT>
+struct BOperand;
+
+// fp16: B = u as a subnormal, u * 2^-24 (exact: u < 2^10); built with one
+// v_perm per register from the code bytes of two consecutive rows.
+template <>
+struct BOperand<F16> {
+  static constexpr float kUnit = 16777216.f;  // 2^24: undoes the subnormal scaling
+  __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta)
+        B[beta][p] = perm(V[2 * p + 1], V[2 * p], 0x0C040C00u + (uint32_t)beta * 0x00010001u);
+  }
+  __device__ __forceinline__ static uint16_t correction(int v) {  // v * 2^-24, |v| < 1024
+    return v >= 0 ? (uint16_t)v : (uint16_t)(0x8000u | (uint32_t)(-v));
+  }
+};
+
+// bf16: B = u (0..255 has at most 8 significant bits, exact in bf16).
+template <>
+struct BOperand<BF16> {
+  static constexpr float kUnit = 1.f;
+  __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta) {
+        const float a = (float)((V[2 * p] >> (8 * beta)) & 0xFFu);
+        const float b = (float)((V[2 * p + 1] >> (8 * beta)) & 0xFFu);
+        B[beta][p] = perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+      }
+    }
+  }
+  __device__ __forceinline__ static uint16_t correction(int v) { return from_f32<BF16>((float)v); }
+};
+
 }  // namespace grinqh

@@ -42,6 +42,16 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N);
 
 int launch_decode(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense,
                   hipStream_t st);
+// y = cast(sum over `splits` of partial[s][M][N]) (+ bias), ranges added in order
+int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream_t st);
+
+constexpr int64_t kTargetBlocks = 256;  // MI355X compute units
+
+// GEMV path (M <= kGemvMaxRows): one word column per lane, 8-row tiles.
+constexpr int64_t kGemvMaxRows = 4;
+// plan.mt is unused; tiles_per_split counts 32-row tiles
+DecodePlan plan_gemv(int64_t M, int64_t K, int64_t N, int64_t group_size);
+int launch_gemv(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense, hipStream_t st);
 int launch_sigma(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* sigma, hipStream_t st);
 
 struct PrefillParams {
