@@ -18,6 +18,7 @@ TFLOP/s at M=2048 (BASELINE configs[2] shapes, dense) and the CPU baseline
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -75,6 +76,34 @@ def decode_bytes(bits_per_row, K, N, M):
     return planes + (K // GS) * N * 2 + M * K * 2 + M * N * 2
 
 
+def kernel_name(M: int, Z: int, dtype: str = "F16", graded: bool = True) -> str:
+    """Kernel instantiation a decode-sweep product of M rows runs (mirrors the
+    library's dispatch: GEMV kernel up to 4 rows, decode kernel above)."""
+    dense = "false" if graded else "true"
+    if M <= 4:
+        return f"gemv_kernel<{dtype},{1 if M == 1 else 4},{Z},{dense}>"
+    mt = 1 if M <= 16 else (2 if M <= 32 else 4)
+    return f"decode_kernel<{dtype},{mt},{Z},{dense}>"
+
+
+def traffic_for(kernel: str):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE (scaled by a copy-kernel calibration), read from
+    the 'traffic:' lines of profiles/*.md; None when not measured."""
+    prof = os.path.join(REPO, "profiles")
+    if not os.path.isdir(prof):
+        return None
+    for f in sorted(os.listdir(prof)):
+        if not f.endswith(".md"):
+            continue
+        with open(os.path.join(prof, f)) as fh:
+            for line in fh:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel:
+                    return int(parts[2])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -83,6 +112,9 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=20, help="launches per case graph for kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="counter-collection run: each decode case twice (eager) and a 256 MiB copy kernel "
+                         "of known traffic for calibrating FETCH_SIZE / WRITE_SIZE; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only: the GRINQH hot path has no sharded path "
@@ -134,6 +166,21 @@ def main() -> int:
             call(c, 0)
     torch.cuda.synchronize()
 
+    if args.pmc_pass:
+        with torch.cuda.stream(stream):
+            for c in cases:
+                for r in range(2):
+                    call(c, 1 + r)
+                torch.cuda.synchronize()
+                log(f"pmc pass: {c['shape']} M={c['M']} kernel {kernel_name(c['M'], BITS // 2)} "
+                    f"bytes {c['bytes']}")
+            src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+            dst = torch.empty_like(src)
+            torch.neg(src, out=dst)  # calibration: reads and writes exactly 256 MiB
+            torch.cuda.synchronize()
+        log("pmc pass: calibration kernel (torch.neg, 256 MiB in, 256 MiB out) done")
+        return 0
+
     # per-case kernel time: graph of `reps` launches cycling the weight copies
     for c in cases:
         g = torch.cuda.CUDAGraph()
@@ -182,15 +229,47 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"step {ms_per_step * 1e3:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s)")
 
-    # dominant kernel: the M<=16 decode kernel instantiation (12 of 16 launches per step)
-    dom = [c for c in cases if c["M"] <= 16]
-    dom_bytes = sum(c["bytes"] for c in dom) / len(dom)
-    dom_us = sum(c["us"] for c in dom) / len(dom)
-    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "grinqh::decode_kernel<F16,1,4,false>", "bytes_per_launch": int(dom_bytes),
-                "avg_launch_us": round(dom_us, 3)}
+    # ---------------- kernel timing: HIP events recorded by the library right
+    # around each product's main kernel (before its split-K reduction), on the
+    # stream the kernel runs on
+    lib = _lib.load_library()
+    ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(args.reps)]
+    with torch.cuda.stream(stream):
+        for a, b in ev_pairs:  # materialise the events before handing them over
+            a.record(stream)
+            b.record(stream)
+    torch.cuda.synchronize()
+    for c in cases:
+        with torch.cuda.stream(stream):
+            for j, (a, b) in enumerate(ev_pairs):
+                _lib.check(lib.grinqh_time_next_product(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event)),
+                           "grinqh_time_next_product")
+                call(c, j % n_copies)
+        torch.cuda.synchronize()
+        c["kernel_us"] = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in ev_pairs]))
+        c["kernel"] = kernel_name(c["M"], BITS // 2)
+    kernels = {}
+    for c in cases:
+        k = kernels.setdefault(c["kernel"], {"launches_per_step": 0, "bytes": 0, "us": 0.0})
+        k["launches_per_step"] += 1
+        k["bytes"] += c["bytes"]
+        k["us"] += c["kernel_us"]
+    for name, k in kernels.items():
+        k["avg_launch_us"] = round(k["us"] / k["launches_per_step"], 3)
+        k["bytes_per_launch"] = int(k["bytes"] / k["launches_per_step"])
+        k["achieved_gbs"] = round(k["bytes"] / (k["us"] * 1e-6) / 1e9, 1)
+        k["frac"] = round(k["achieved_gbs"] / HBM_PEAK_GBS, 4)
+        k["share_of_step"] = round(k["us"] * 1e-3 / ms_per_step, 4)
+        log(f"{name:40s} x{k['launches_per_step']} avg {k['avg_launch_us']:8.2f} us "
+            f"{k['achieved_gbs']:8.1f} GB/s ({100 * k['frac']:.1f}% HBM) share {100 * k['share_of_step']:.1f}%")
+    dom_name = max(kernels, key=lambda n: kernels[n]["us"])
+    dom = kernels[dom_name]
+    roofline = {"bound": "hbm", "achieved": dom["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": dom["frac"], "traffic": traffic_for(dom_name), "kernel": "grinqh::" + dom_name,
+                "bytes_per_launch": dom["bytes_per_launch"], "avg_launch_us": dom["avg_launch_us"]}
+    for k in kernels.values():
+        del k["us"], k["bytes"]
 
     # ---------------- prefill at M=2048 (dense dequantize-then-matmul, reference dispatch for M>1)
     prefill = None
@@ -248,6 +327,7 @@ def main() -> int:
                                "M=1,4,16,64, union grading t=[0,P50,P80,P95], max_bits 8, group 128",
                    "weight_copies": n_copies, "frac_of_hbm_roofline": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
+        "kernels": kernels,
         "cpu_baseline": cpu,
         "cases": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in c.items() if k not in ("x", "t")}
                   for c in cases],

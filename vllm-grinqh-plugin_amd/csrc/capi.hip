@@ -2,6 +2,8 @@
 // argument validation, workspace carving and kernel selection.
 #include <string.h>
 
+#include <mutex>
+
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 
@@ -18,6 +20,13 @@ inline bool valid_bits(int b) { return b == 2 || b == 4 || b == 6 || b == 8; }
 inline bool valid_dtype(int d) { return d == GRINQH_DTYPE_F16 || d == GRINQH_DTYPE_BF16; }
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// One-shot kernel timing events (grinqh_time_next_product).
+struct KernelEvents {
+  std::mutex mu;
+  hipEvent_t before = nullptr, after = nullptr;
+};
+KernelEvents g_events;
 
 struct WorkspaceLayout {
   size_t sigma_off, partial_off, total;
@@ -108,9 +117,23 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
     p.M = (int)mc;
     p.splits = plan.splits;
     p.tiles_per_split = plan.tiles_per_split;
+    hipEvent_t ev_after = nullptr;
+    if (m0 == 0) {
+      std::lock_guard<std::mutex> lock(g_events.mu);
+      if (g_events.before != nullptr) {
+        if (hipEventRecord(g_events.before, st) != hipSuccess) return GRINQH_ERR_HIP;
+        ev_after = g_events.after;
+        g_events.before = g_events.after = nullptr;
+      }
+    }
     rc = mc <= kGemvMaxRows ? launch_gemv(p, plan, max_bits, dtype, !graded, st)
                             : launch_decode(p, plan, max_bits, dtype, !graded, st);
     if (rc != GRINQH_OK) return rc;
+    if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
+    if (plan.splits > 1) {
+      rc = launch_splitk_reduce(p, plan.splits, dtype, st);
+      if (rc != GRINQH_OK) return rc;
+    }
   }
   return GRINQH_OK;
 }
@@ -212,6 +235,14 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
                          int group_size, void* workspace, size_t workspace_bytes, void* stream) {
   return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, nullptr,
                      GRINQH_MODE_DENSE, workspace, workspace_bytes, stream);
+}
+
+int grinqh_time_next_product(void* event_before, void* event_after) {
+  if ((event_before == nullptr) != (event_after == nullptr)) return GRINQH_ERR_INVALID;
+  std::lock_guard<std::mutex> lock(g_events.mu);
+  g_events.before = static_cast<hipEvent_t>(event_before);
+  g_events.after = static_cast<hipEvent_t>(event_after);
+  return GRINQH_OK;
 }
 
 }  // extern "C"

@@ -471,7 +471,6 @@ int launch_decode(const DecodeParams& p, const DecodePlan& pl, int max_bits, int
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_decode_dt<BF16>(p, pl, Z, dense, st)
                                             : launch_decode_dt<F16>(p, pl, Z, dense, st);
   if (rc != GRINQH_OK) return rc;
-  if (pl.splits > 1) return launch_splitk_reduce(p, pl.splits, dtype, st);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

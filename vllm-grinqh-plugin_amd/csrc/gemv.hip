@@ -343,7 +343,6 @@ int launch_gemv(const DecodeParams& p, const DecodePlan& pl, int max_bits, int d
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_gemv_dt<BF16>(p, pl, Z, dense, st)
                                             : launch_gemv_dt<F16>(p, pl, Z, dense, st);
   if (rc != GRINQH_OK) return rc;
-  if (pl.splits > 1) return launch_splitk_reduce(p, pl.splits, dtype, st);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

@@ -40,6 +40,7 @@ struct DecodePlan {
 
 DecodePlan plan_decode(int64_t M, int64_t K, int64_t N);
 
+// Main kernels only: when plan.splits > 1 the caller follows with launch_splitk_reduce.
 int launch_decode(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense,
                   hipStream_t st);
 // y = cast(sum over `splits` of partial[s][M][N]) (+ bias), ranges added in order

@@ -47,6 +47,7 @@ SIGNATURES = {
                                        _vp, ctypes.c_size_t, _vp]),
     "grinqh_prefill_dense": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32,
                                     _vp, ctypes.c_size_t, _vp]),
+    "grinqh_time_next_product": (_i32, [_vp, _vp]),
 }
 
 _lock = threading.Lock()
