@@ -31,6 +31,20 @@ def dense_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, dtype:
     return u * (np.abs(np.asarray(x, dtype=np.float64)) @ (np.abs(W.astype(np.float64)) * s))
 
 
+def graded_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, thresholds, max_bits: int, dtype: str,
+                          group_size: int = 128):
+    """The same bound for a union-graded product whose kernel rounds the
+    effective weight w_eff*s to the activation dtype (the prefill kernel for
+    batches above 64 rows): u * (|x| @ |w_eff*s|), w_eff from the union grade."""
+    from oracle import grinqh_oracle as O
+    u = UNIT_ROUNDOFF[dtype]
+    xa = np.abs(np.asarray(x, dtype=np.float64))
+    sigma = np.abs(np.asarray(x, dtype=np.float32)).max(0)
+    weff = O.effective_weight(W, O.grade(sigma, thresholds, max_bits), max_bits).astype(np.float64)
+    s = np.repeat(np.abs(np.asarray(scale, dtype=np.float64)), group_size, axis=0)[: W.shape[0]]
+    return u * (xa @ (np.abs(weff) * s))
+
+
 def output_tolerance(ref_pre: np.ndarray, dtype: str, bias=None) -> np.ndarray:
     """Allowed |y - y_ref| for a kernel output against the float64 oracle.
 

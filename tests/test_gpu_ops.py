@@ -13,7 +13,8 @@ import pytest
 import torch
 
 from oracle import grinqh_oracle as O
-from tests._helpers import TORCH_DTYPES, assert_output_close, dense_rounding_bound, rand_weight, to_dtype_np
+from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound, graded_rounding_bound,
+                            rand_weight, to_dtype_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -219,7 +220,40 @@ def test_union_graded_batches(M, max_bits, dtype):
     t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128, 192, t)
     pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
-    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, max_bits, 128, dtype), dtype, what=f"union M={M}")
+    # above 64 rows the prefill kernel rounds w_eff*s to the activation dtype
+    extra = graded_rounding_bound(x, W, s, t, max_bits, dtype) if M > 64 else None
+    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, max_bits, 128, dtype), dtype, what=f"union M={M}",
+                        extra_tol=extra)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+@pytest.mark.parametrize("M,K,N", [(65, 256, 320), (300, 512, 768), (129, 96, 4112)])
+def test_prefill_dense_shapes(M, K, N, max_bits, dtype):
+    """Prefill kernel (more than 64 rows) against S9 with bias: partial row
+    tiles, column blocks cut short (N/16 not a multiple of 16), K of 3 stages."""
+    from grinqh.kernel import run_product
+    rng = np.random.default_rng(M + K + N + max_bits)
+    W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    y = run_product(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), _tdt(bias, dtype), max_bits, 128,
+                    N // 4, [0.0] * 4, "dense")
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, bias, 128, dtype), dtype, bias=bias,
+                        what=f"prefill {M}x{K}x{N}", extra_tol=dense_rounding_bound(x, W, s, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_256_row_tiles(dtype):
+    """Enough blocks for the 256-row tile variant (64 column blocks x 4 row tiles)."""
+    from grinqh.kernel import grinqh_prefill_dense
+    M, K, N = 1000, 256, 16384
+    rng = np.random.default_rng(77)
+    W, x, s = _setup(rng, K, N, 8, dtype, M=M)
+    y = grinqh_prefill_dense(_tdt(x, dtype), _prepare(W, 8), _tdt(s, dtype), 128, N // 4, 8)
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="prefill 256-row tiles",
+                        extra_tol=dense_rounding_bound(x, W, s, dtype))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

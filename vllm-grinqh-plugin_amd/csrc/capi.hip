@@ -42,13 +42,10 @@ DecodePlan plan_launch(int64_t mc, int64_t K, int64_t N, int64_t group_size) {
 // [sigma (K floats, union batches split into several launches) | split-K partials]
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
-  const int64_t m_launch = M < kDecodeMaxRows ? M : kDecodeMaxRows;
-  w.plan = plan_launch(m_launch > 0 ? m_launch : 1, K, N, 32);
-  size_t partial = w.plan.splits > 1 ? w.plan.workspace : 0;
-  if (M > kDecodeMaxRows && M % kDecodeMaxRows != 0) {  // the last, shorter launch may split differently
-    const DecodePlan tail = plan_launch(M % kDecodeMaxRows, K, N, 32);
-    const size_t tail_partial = tail.splits > 1 ? tail.workspace : 0;
-    if (tail_partial > partial) partial = tail_partial;
+  size_t partial = 0;
+  if (M <= kDecodeMaxRows) {  // larger batches run the prefill kernel, which needs no partial sums
+    w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
+    partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   }
   const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kDecodeMaxRows;
   w.sigma_off = 0;
@@ -68,6 +65,45 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
   if (!aligned(y, 8) || !aligned(scale, 2)) return GRINQH_ERR_INVALID;
   // plane words are addressed with 32-bit byte offsets (bit 31 reserved)
   if (K * (max_bits / 2) * (N / 16) * 4 >= ((int64_t)1 << 31)) return GRINQH_ERR_INVALID;
+  return GRINQH_OK;
+}
+
+// M > kDecodeMaxRows: one prefill launch over the whole batch (graded batches
+// first reduce the union statistic over all M rows).
+int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
+                bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
+  PrefillParams p{};
+  p.x = xs;
+  p.ldx = d.ldx;
+  p.planes = d.planes;
+  p.scale = d.scale;
+  p.bias = d.bias;
+  p.y = ys;
+  p.thr = d.thr;
+  p.M = (int)M;
+  p.K = d.K;
+  p.N = d.N;
+  p.NW = d.NW;
+  p.gs = d.gs;
+  p.sigma = nullptr;
+  if (graded) {
+    float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
+    const int rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
+    if (rc != GRINQH_OK) return rc;
+    p.sigma = sigma;
+  }
+  hipEvent_t ev_after = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_events.mu);
+    if (g_events.before != nullptr) {
+      if (hipEventRecord(g_events.before, st) != hipSuccess) return GRINQH_ERR_HIP;
+      ev_after = g_events.after;
+      g_events.before = g_events.after = nullptr;
+    }
+  }
+  const int rc = launch_prefill(p, max_bits, dtype, !graded, st);
+  if (rc != GRINQH_OK) return rc;
+  if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
   return GRINQH_OK;
 }
 
@@ -103,12 +139,7 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
 
   const uint16_t* xs = static_cast<const uint16_t*>(x);
   uint16_t* ys = static_cast<uint16_t*>(y);
-  if (graded && M > kDecodeMaxRows) {
-    float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
-    rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sigma, st);
-    if (rc != GRINQH_OK) return rc;
-    p.sigma = sigma;
-  }
+  if (M > kDecodeMaxRows) return run_prefill(p, xs, ys, M, dtype, max_bits, graded, ws, wl, st);
   for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
     const DecodePlan plan = plan_launch(mc, K, N, group_size);

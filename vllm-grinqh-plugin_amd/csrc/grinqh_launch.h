@@ -64,9 +64,12 @@ struct PrefillParams {
   uint16_t* y;
   GradeThresholds thr;
   int M, K, N, NW, gs;
+  const float* sigma;  // union statistic [K] (graded mode), else nullptr
 };
 
+// Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.
 int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st);
+int prefill_block_rows(int64_t M, int64_t N);
 
 int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
 int launch_prepare_weight(const int8_t* W, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
