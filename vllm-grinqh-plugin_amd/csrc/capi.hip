@@ -12,7 +12,8 @@ using namespace grinqh;
 namespace {
 
 constexpr int kAbiVersion = 1;
-constexpr int64_t kDecodeMaxRows = 64;  // rows handled by one decode launch
+constexpr int64_t kDecodeMaxRows = 64;     // rows handled by one decode launch
+constexpr int64_t kSigmaPrepassRows = 16;  // graded batches above this reduce sigma in a pre-pass
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -38,6 +39,11 @@ struct WorkspaceLayout {
 DecodePlan plan_launch(int64_t mc, int64_t K, int64_t N, int64_t group_size) {
   return mc <= kGemvMaxRows ? plan_gemv(mc, K, N, group_size) : plan_decode(mc, K, N);
 }
+int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense,
+                hipStream_t st) {
+  return p.M <= kGemvMaxRows ? launch_gemv(p, plan, max_bits, dtype, dense, st)
+                             : launch_decode(p, plan, max_bits, dtype, dense, st);
+}
 
 // [sigma (K floats, union batches split into several launches) | split-K partials]
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
@@ -47,7 +53,7 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
     w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
     partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   }
-  const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kDecodeMaxRows;
+  const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kSigmaPrepassRows;
   w.sigma_off = 0;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
@@ -140,6 +146,12 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   const uint16_t* xs = static_cast<const uint16_t*>(x);
   uint16_t* ys = static_cast<uint16_t*>(y);
   if (M > kDecodeMaxRows) return run_prefill(p, xs, ys, M, dtype, max_bits, graded, ws, wl, st);
+  if (graded && M > kSigmaPrepassRows) {  // decode above 16 rows grades from the batch statistic
+    float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
+    rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sigma, st);
+    if (rc != GRINQH_OK) return rc;
+    p.sigma = sigma;
+  }
   for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
     const DecodePlan plan = plan_launch(mc, K, N, group_size);
@@ -157,8 +169,7 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
         g_events.before = g_events.after = nullptr;
       }
     }
-    rc = mc <= kGemvMaxRows ? launch_gemv(p, plan, max_bits, dtype, !graded, st)
-                            : launch_decode(p, plan, max_bits, dtype, !graded, st);
+    rc = launch_main(p, plan, max_bits, dtype, !graded, st);
     if (rc != GRINQH_OK) return rc;
     if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
     if (plan.splits > 1) {

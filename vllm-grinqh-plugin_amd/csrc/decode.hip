@@ -48,15 +48,20 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   constexpr int NJ = 4 / MT;   // output dwords j per wave
   constexpr int KW = 4 / MT;   // K sub-ranges per block
   constexpr int SH = 8 - 2 * Z;
-  constexpr int RMAX = kDecodeRowsPerBlock / MT;
+  // Up to 16 rows x is staged in LDS for the block's K range; above that the
+  // A operand is read from global memory (L2-resident) with the plane words,
+  // and grading uses the batch statistic computed beforehand, so the K range
+  // is not limited by staging x.
+  constexpr bool AG = MT >= 2;
+  constexpr int RMAX = AG ? kDecodeRowsPerBlock : kDecodeRowsPerBlock / MT;
   constexpr int XS = RMAX + 8;  // halves per staged x row (16-byte rows, banks staggered)
-  constexpr int X_BYTES = MP * XS * 2;
+  constexpr int X_BYTES = AG ? 0 : MP * XS * 2;
   constexpr int OFF_BYTES = RMAX * Z * 4;
   constexpr int RED_VECS = (KW - 1) * MT * 16 * 64;  // f32x4 slots for the in-block reduction
   constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_VECS * 16 ? (X_BYTES + OFF_BYTES) : RED_VECS * 16;
   constexpr int SC_GROUPS = RMAX / 32 + 1;  // scale groups a K range can touch (group size >= 32)
   constexpr int CPR = RMAX / 8;             // 16-byte x chunks per staged row
-  constexpr int XPT = MP * CPR / 256;       // x chunks per thread
+  constexpr int XPT = AG ? 1 : MP * CPR / 256;  // x chunks per thread
   constexpr int SPT = (SC_GROUPS * 32 + 255) / 256;  // 16-byte scale chunks per thread
 
   // staging area: x rows and (row, plane) offsets; reused for the in-block reduction
@@ -95,12 +100,13 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     u32x4_t xv[XPT];
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
+      if constexpr (AG) break;
       const int m = mb + k * (256 / CPR);
       const uint32_t off =
           (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
       xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
-    const bool vec_scales = (p.NW % 8) == 0;
+    const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
     u32x4_t sv[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
@@ -112,10 +118,12 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
               : 0x80000000u;
       sv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(sr, (int)off, 0, 0));
     }
+    if constexpr (!AG) {
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) {
-      const int m = mb + k * (256 / CPR);
-      *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
+      for (int k = 0; k < XPT; ++k) {
+        const int m = mb + k * (256 / CPR);
+        *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
+      }
     }
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
@@ -143,7 +151,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       bits = (1u << Z) - 1u;
     } else {
       float s;
-      if (p.sigma != nullptr) {
+      if (AG || p.sigma != nullptr) {  // batch statistic computed beforehand (always above 16 rows)
         s = p.sigma[row0 + rr];
       } else {
         s = fabsf(to_f32<DT>(s_x[rr]));
@@ -193,7 +201,16 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   const uint32_t lane_off = (uint32_t)wc * 4u;
 
   typedef uint32_t offz_t __attribute__((ext_vector_type(Z)));
-  auto issue = [&](int t, uint32_t (&D)[8][Z]) {
+  // plane words of one tile (and, above 16 rows, its A operand)
+  struct Tile {
+    uint32_t D[8][Z];
+    u32x4_t A[AG ? MT : 1];
+  };
+  const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xsrc_none =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), (short)0, 0, 0x00020000);
+  auto issue = [&](int t, Tile& T) {
     const bool live = t < t_end;
     const __amdgpu_buffer_rsrc_t rs = live ? prsrc : prsrc_none;
     const int sb = (live ? t : t_begin) * 32 + 8 * q;
@@ -208,34 +225,48 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int z = 0; z < Z; ++z) {
         const uint32_t oz = (Z == 1) ? (uint32_t)o[0] : (uint32_t)o[z];
-        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
+        T.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
+      }
+    }
+    if constexpr (AG) {  // x[16*mt + c][rows 8q .. 8q+7 of the tile]; rows m >= M read 0
+      const __amdgpu_buffer_rsrc_t xs = live ? xsrc : xsrc_none;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + c;
+        const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + sb) * 2) : 0x80000000u;
+        T.A[mt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xs, (int)off, 0, 0));
       }
     }
   };
 
   // one tile: optional prefetch of tile t+2, unpack, MFMA, group epilogue
-  auto step = [&](int t, uint32_t (&Dc)[8][Z], bool prefetch, uint32_t (&Dn)[8][Z]) {
+  auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn) {
     const int gt = tile0 + t;  // absolute tile
     const bool first_of_group = (t == t_begin) || (gt % tiles_per_group == 0);
     const bool last_of_group = (t + 1 == t_end) || ((gt + 1) % tiles_per_group == 0);
-    if (prefetch) issue(t + 2, Dn);
+    if (prefetch) issue(t + 2, Tn);
     __builtin_amdgcn_sched_barrier(0);
 
     const int sb = t * 32 + 8 * q;
     const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[sb]);
 
-    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile] from LDS
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile]
     u32x4_t A[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (AG)
+        A[mt] = Tc.A[mt];
+      else
+        A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
+    }
 
     // Rebuild the code bytes (offset binary) and turn them into B operands.
-    prepare_planes<Z>(Dc);
+    prepare_planes<Z>(Tc.D);
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
       const int j = jg * NJ + jj;
       uint32_t V[8];
-      code_dwords<Z>(Dc, j, V);
+      code_dwords<Z>(Tc.D, j, V);
       u32x4_t B[4];
       BOperand<DT>::build(V, B);
       // the first tile of a scale group starts its sums from zero
@@ -272,18 +303,18 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 
   {
     // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
-    uint32_t DA[8][Z], DB[8][Z], DC[8][Z];
-    issue(t_begin, DA);
-    issue(t_begin + 1, DB);
+    Tile TA, TB, TC;
+    issue(t_begin, TA);
+    issue(t_begin + 1, TB);
     int t = t_begin;
     for (; t + 3 <= t_end; t += 3) {
-      step(t, DA, true, DC);
-      step(t + 1, DB, true, DA);
-      step(t + 2, DC, true, DB);
+      step(t, TA, true, TC);
+      step(t + 1, TB, true, TA);
+      step(t + 2, TC, true, TB);
     }
-    // at most two tiles left, already loaded into DA and DB
-    if (t < t_end) step(t, DA, false, DC);
-    if (t + 1 < t_end) step(t + 1, DB, false, DC);
+    // at most two tiles left, already loaded into TA and TB
+    if (t < t_end) step(t, TA, false, TC);
+    if (t + 1 < t_end) step(t + 1, TB, false, TC);
   }
 
   // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...
@@ -408,7 +439,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   pl.col_blocks = (int)((NW + 15) / 16);
   const int64_t T = K / 32;
   const int kw = 4 / pl.mt;
-  const int64_t tiles_max = kDecodeRowsPerBlock / pl.mt / 32;
+  const int64_t tiles_max = (pl.mt >= 2 ? kDecodeRowsPerBlock : kDecodeRowsPerBlock / pl.mt) / 32;
   const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
   // one block per CU, all blocks resident at once: the per-block set-up
   // (staging, grading) is paid once per CU rather than once per round
