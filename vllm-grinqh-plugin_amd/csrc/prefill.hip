@@ -28,7 +28,6 @@ namespace grinqh {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kPrefillKP = 40;  // halves per LDS row of a 32-row stage (32 + 8 pad: conflict-free)
 
 // Two rows (low half = row 0, high half = row 1) of column tile beta from the
 // code dwords V0, V1 (offset-binary bytes u): RNE(w * s) with
@@ -61,32 +60,39 @@ struct Dequant<BF16, SH> {
   }
 };
 
-template <typename DT, int BM, int Z, bool DENSE>
-__global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
+// One block: BM rows x 256 logical columns; WAVES waves as (WAVES/2) x 2, each
+// BM/(WAVES/2) rows x 8 column tiles.  A stage is BK rows of K: its global
+// loads are issued before the previous stage's MFMAs and consumed after them,
+// so a longer stage hides more load latency.  Each dequantizing thread owns one
+// word column, BK/16 rows and 4*JPT column tiles.
+template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK>
+__global__ __launch_bounds__(WAVES * 64, 1) void prefill_kernel(PrefillParams p) {
+  constexpr int NT = WAVES * 64;
   constexpr int SH = 8 - 2 * Z;
-  constexpr int KP = kPrefillKP;
-  constexpr int WM = BM / 2;       // rows per wave
-  constexpr int MTW = WM / 16;     // 16-row MFMA tiles per wave
-  constexpr int A_HALVES = BM * KP;
-  constexpr int B_HALVES = 256 * KP;  // (column tile, column) rows of 32 k
-  constexpr int AL = BM * 4 / 256;    // 16-byte A chunks per thread per stage
+  constexpr int KP = BK + 8;        // halves per LDS row (padding: conflict-free fragment reads)
+  constexpr int WGM = WAVES / 2;    // waves along M (2 along N)
+  constexpr int WM = BM / WGM;      // rows per wave
+  constexpr int MTW = WM / 16;      // 16-row MFMA tiles per wave
+  constexpr int CPR = BK / 8;       // 16-byte x chunks per row per stage
+  constexpr int AL = BM * CPR / NT;
+  constexpr int RPT = BK / 16;      // rows per dequantizing thread
+  constexpr int JPT = 4 * 256 / NT; // output dwords j per dequantizing thread
+  static_assert(MTW >= 1 && AL >= 1 && RPT % 2 == 0 && JPT >= 1, "tile shape");
 
-  __shared__ __align__(16) uint16_t s_a[2][A_HALVES];
-  __shared__ __align__(16) uint16_t s_b[2][B_HALVES];
+  __shared__ __align__(16) uint16_t s_a[2][BM * KP];
+  __shared__ __align__(16) uint16_t s_b[2][256 * KP];  // (column tile, column) rows of BK k
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WGM, wn = wave / WGM;
   const int c = lane & 15, q = lane >> 4;
   const int w0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * BM;
-  const int nstages = p.K >> 5;
+  const int nstages = p.K / BK;
 
-  // A loader: chunk (row, 16-byte piece): 4 threads per row
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
-  // B loader: word column wcol, rows 2*rp and 2*rp + 1 of the stage
-  const int wcol = tid & 15, rp = tid >> 4;
+  const int wcol = tid & 15, rg = (tid >> 4) & 15, j0 = (tid >> 8) * JPT;
   const bool col_ok_ld = (w0 + wcol) < p.NW;
   const int wc_ld = col_ok_ld ? (w0 + wcol) : (p.NW - 1);
   const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -94,56 +100,55 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
   const uint32_t plane_row_bytes = (uint32_t)(Z * p.NW) * 4u;
 
   u32x4_t xa[AL];
-  uint32_t D[2][Z];
-  float sig[2];
-  uint16_t sraw[16];  // scales of the stage's group when it starts a new group
+  uint32_t D[RPT][Z];
+  float sig[RPT];
+  uint16_t sraw[4 * JPT];  // scales of the stage's group when it starts a new group
   bool new_group = false;
   auto load_stage = [&](int s) {
-    const int k0 = s * 32;
-    new_group = (s == 0) || (k0 / p.gs != (k0 - 32) / p.gs);
-    if (new_group) {  // this thread's 16 columns: column tile r, word column wc_ld
+    const int k0 = s * BK;
+    new_group = (s == 0) || (k0 / p.gs != (k0 - BK) / p.gs);
+    if (new_group) {  // this thread's columns: column tiles 4*j0 .., word column wc_ld
       const int g = k0 / p.gs;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sraw[r] = p.scale[(int64_t)g * p.N + (int64_t)r * p.NW + wc_ld];
+      for (int r = 0; r < 4 * JPT; ++r) sraw[r] = p.scale[(int64_t)g * p.N + (int64_t)(4 * j0 + r) * p.NW + wc_ld];
     }
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const int h = tid + 256 * i, row = h >> 2, piece = h & 3;
+      const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
       const int m = m0 + row;
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + k0 + 8 * piece) * 2) : 0x80000000u;
       xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint32_t rb = (uint32_t)(k0 + 2 * rp + e) * plane_row_bytes + (uint32_t)wc_ld * 4u;
+    for (int e = 0; e < RPT; ++e) {
+      const int row = k0 + rg * RPT + e;
+      const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
 #pragma unroll
       for (int z = 0; z < Z; ++z)
         D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
-      if (!DENSE) sig[e] = p.sigma[k0 + 2 * rp + e];
+      if (!DENSE) sig[e] = p.sigma[row];
     }
   };
 
-  // scales of this thread's 16 columns for the current group
-  uint32_t s2[16];  // fp16: (s, s)
-  float sf[16];     // bf16: s * 2^-sh
+  uint32_t s2[4 * JPT];  // fp16: (s, s)
+  float sf[4 * JPT];     // bf16: s * 2^-sh
 
+  // x rows as they are; B: grade (union), rebuild code bytes, RNE(w * s),
+  // written as (column tile, column)[k]
   auto store_stage = [&](int buf) {
-    // A: straight copy
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const int h = tid + 256 * i, row = h >> 2, piece = h & 3;
+      const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
       *reinterpret_cast<u32x4_t*>(&s_a[buf][row * KP + 8 * piece]) = xa[i];
     }
-    // B: grade (union), rebuild code bytes, dequantize, write (column tile, column)[k]
-    uint32_t bits[2];
-    int beta[2];
+    int beta[RPT];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      bits[e] = DENSE ? ((1u << Z) - 1u) : zone_bits<Z>(sig[e], p.thr.t);
-      beta[e] = DENSE ? 0 : midpoint_bias<Z>(bits[e]);
+    for (int e = 0; e < RPT; ++e) {
+      const uint32_t bits = DENSE ? ((1u << Z) - 1u) : zone_bits<Z>(sig[e], p.thr.t);
+      beta[e] = DENSE ? 0 : midpoint_bias<Z>(bits);
       if (!DENSE) {
 #pragma unroll
-        for (int z = 0; z < Z; ++z) D[e][z] &= ((bits[e] >> z) & 1u) ? 0xFFFFFFFFu : 0u;
+        for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((bits >> z) & 1u);
       }
       D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U & mask) + 128
 #pragma unroll
@@ -151,45 +156,50 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     }
     if (new_group) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 4 * JPT; ++r) {
         if constexpr (DT::id == F16::id)
           s2[r] = (uint32_t)sraw[r] | ((uint32_t)sraw[r] << 16);
         else
           sf[r] = to_f32<DT>(sraw[r]) * (1.0f / (float)(1 << SH));
       }
     }
-    uint32_t negc = 0;
-    float cb[2] = {0.f, 0.f};
-    if constexpr (DT::id == F16::id) {
-      const uint16_t c0 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[0]));
-      const uint16_t c1 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[1]));
-      negc = (uint32_t)c0 | ((uint32_t)c1 << 16);
-    } else {
-      cb[0] = (float)(128 - beta[0] * (1 << SH));
-      cb[1] = (float)(128 - beta[1] * (1 << SH));
-    }
-    uint16_t* bdst = &s_b[buf][wcol * KP + 2 * rp];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t V[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        uint32_t h = (Z == 4) ? D[e][3] : (D[e][0] & (0x03030303u << (2 * ((3 - j) & 3))));
-#pragma unroll
-        for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
-          h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), D[e][z], h);
-        V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
+    for (int pp = 0; pp < RPT / 2; ++pp) {
+      uint32_t negc = 0;
+      float cb0 = 0.f, cb1 = 0.f;
+      if constexpr (DT::id == F16::id) {
+        const uint16_t c0 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[2 * pp]));
+        const uint16_t c1 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[2 * pp + 1]));
+        negc = (uint32_t)c0 | ((uint32_t)c1 << 16);
+      } else {
+        cb0 = (float)(128 - beta[2 * pp] * (1 << SH));
+        cb1 = (float)(128 - beta[2 * pp + 1] * (1 << SH));
       }
+      uint16_t* bdst = &s_b[buf][wcol * KP + rg * RPT + 2 * pp];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int r = 4 * j + b;
-        uint32_t pr;
-        if constexpr (DT::id == F16::id) {
-          pr = Dequant<F16, SH>::pair(V[0], V[1], b, negc, s2[r]);
-        } else {
-          pr = Dequant<BF16, SH>::pair_bf16(V[0], V[1], b, cb[0], cb[1], sf[r]);
+      for (int jj = 0; jj < JPT; ++jj) {
+        const int j = j0 + jj;
+        uint32_t V[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int ee = 2 * pp + e;
+          uint32_t h = (Z == 4) ? D[ee][3] : (D[ee][0] & (0x03030303u << (2 * ((3 - j) & 3))));
+#pragma unroll
+          for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
+            h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), D[ee][z], h);
+          V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
         }
-        *reinterpret_cast<uint32_t*>(bdst + r * 16 * KP) = pr;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int r = 4 * j + b;
+          uint32_t pr;
+          if constexpr (DT::id == F16::id) {
+            pr = Dequant<F16, SH>::pair(V[0], V[1], b, negc, s2[4 * jj + b]);
+          } else {
+            pr = Dequant<BF16, SH>::pair_bf16(V[0], V[1], b, cb0, cb1, sf[4 * jj + b]);
+          }
+          *reinterpret_cast<uint32_t*>(bdst + r * 16 * KP) = pr;
+        }
       }
     }
   };
@@ -206,16 +216,27 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
   for (int s = 0; s < nstages; ++s) {
     const int buf = s & 1;
     if (s + 1 < nstages) load_stage(s + 1);
-    // B fragments of this wave's 8 column tiles, then the A tiles one by one
-    u32x4_t Bf[8];
+    // All fragments of a 32-deep k step are read before its MFMAs, and the
+    // next k step's fragments are read while they run, so the matrix core is
+    // not left waiting on LDS between tiles.
+    u32x4_t Bf[2][8], Af[2][MTW];
+    auto read_frags = [&](int ks, int f) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
-      Bf[r] = *reinterpret_cast<const u32x4_t*>(&s_b[buf][((8 * wn + r) * 16 + c) * KP + 8 * q]);
+      for (int r = 0; r < 8; ++r)
+        Bf[f][r] = *reinterpret_cast<const u32x4_t*>(&s_b[buf][((8 * wn + r) * 16 + c) * KP + 32 * ks + 8 * q]);
 #pragma unroll
-    for (int i = 0; i < MTW; ++i) {
-      const u32x4_t Af = *reinterpret_cast<const u32x4_t*>(&s_a[buf][(wm * WM + 16 * i + c) * KP + 8 * q]);
+      for (int i = 0; i < MTW; ++i)
+        Af[f][i] = *reinterpret_cast<const u32x4_t*>(&s_a[buf][(wm * WM + 16 * i + c) * KP + 32 * ks + 8 * q]);
+    };
+    read_frags(0, 0);
 #pragma unroll
-      for (int r = 0; r < 8; ++r) acc[i][r] = mfma16x16x32<DT>(Af, Bf[r], acc[i][r]);
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      if (ks + 1 < BK / 32) read_frags(ks + 1, (ks + 1) & 1);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+      for (int i = 0; i < MTW; ++i)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) acc[i][r] = mfma16x16x32<DT>(Af[ks & 1][i], Bf[ks & 1][r], acc[i][r]);
     }
     if (s + 1 < nstages) store_stage(buf ^ 1);
     __syncthreads();
@@ -237,22 +258,22 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(PrefillParams p) {
     }
 }
 
-template <typename DT, int BM, int Z>
+template <typename DT, int BM, int Z, int WAVES, int BK>
 static void launch_prefill_t(const PrefillParams& p, bool dense, hipStream_t st) {
   const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM);
   if (dense)
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK>), grid, dim3(WAVES * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK>), grid, dim3(WAVES * 64), 0, st, p);
 }
 
-template <typename DT, int BM>
+template <typename DT, int BM, int WAVES, int BK>
 static int launch_prefill_bm(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
   switch (Z) {
-    case 1: launch_prefill_t<DT, BM, 1>(p, dense, st); break;
-    case 2: launch_prefill_t<DT, BM, 2>(p, dense, st); break;
-    case 3: launch_prefill_t<DT, BM, 3>(p, dense, st); break;
-    case 4: launch_prefill_t<DT, BM, 4>(p, dense, st); break;
+    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK>(p, dense, st); break;
+    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK>(p, dense, st); break;
+    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK>(p, dense, st); break;
+    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK>(p, dense, st); break;
     default: return GRINQH_ERR_INVALID;
   }
   return GRINQH_OK;
@@ -264,10 +285,18 @@ int prefill_block_rows(int64_t M, int64_t N) {
   return col_blocks * ((M + 255) / 256) >= kTargetBlocks ? 256 : 128;
 }
 
+// 64-row stages when K and the group size allow (more load latency hidden per
+// stage), else 32-row stages.
 template <typename DT>
 static int launch_prefill_dt(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
-  return prefill_block_rows(p.M, p.N) == 256 ? launch_prefill_bm<DT, 256>(p, Z, dense, st)
-                                             : launch_prefill_bm<DT, 128>(p, Z, dense, st);
+  // 256-row tiles: one wave per SIMD (128 x 128 per wave); 128-row tiles: two
+  // waves per SIMD (32 x 128 per wave), whose dequantization and MFMAs overlap.
+  const bool bk64 = (p.K % 64 == 0) && (p.gs % 64 == 0);
+  if (prefill_block_rows(p.M, p.N) == 256)
+    return bk64 ? launch_prefill_bm<DT, 256, 4, 64>(p, Z, dense, st)
+                : launch_prefill_bm<DT, 256, 4, 32>(p, Z, dense, st);
+  return bk64 ? launch_prefill_bm<DT, 128, 8, 64>(p, Z, dense, st)
+              : launch_prefill_bm<DT, 128, 8, 32>(p, Z, dense, st);
 }
 
 int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st) {
