@@ -67,6 +67,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   // staging area: x rows and (row, plane) offsets; reused for the in-block reduction
   __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
   __shared__ __align__(16) uint16_t s_bv[RMAX];    // row -> correction-column value
+  __shared__ __align__(16) uint32_t s_xm[RMAX];    // row -> zone-0 flip
   __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
@@ -140,11 +141,12 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   }
   __syncthreads();
 
-  // ---- phase 1b: grade each row: correction-column value and plane offsets
-  // The code bytes are consumed in offset binary: zone 0's digits are flipped
-  // for every row (also rows whose zone 0 is inactive and reads as zero), so
-  // the byte is u = int8(U & mask) + 128 and the column value removes the 128:
-  //   w_eff * 2^sh = u + (beta * 2^sh - 128).
+  // ---- phase 1b: grade each row: correction-column value, zone-0 flip and
+  // plane offsets.  Rows with zone 0 active are consumed in offset binary (zone
+  // 0's digits flipped, u = int8(U & mask) + 128, and the column value removes
+  // the 128); other rows have bit 7 clear and need no flip:
+  //   w_eff * 2^sh = u + beta * 2^sh - (zone 0 active ? 128 : 0).
+  // A row with no active zone therefore contributes exact zeros.
   for (int rr = tid; rr < R; rr += 256) {
     uint32_t bits;
     if (DENSE) {
@@ -160,7 +162,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       bits = zone_bits<Z>(s, p.thr.t);
     }
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
-    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - 128);
+    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - ((bits & 1u) ? 128 : 0));
+    s_xm[rr] = zone0_flip(bits);
     const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
 #pragma unroll
     for (int z = 0; z < Z; ++z)
@@ -261,7 +264,17 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     }
 
     // Rebuild the code bytes (offset binary) and turn them into B operands.
-    prepare_planes<Z>(Tc.D);
+    uint32_t xm[8];
+    {
+      const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&s_xm[sb]);
+      const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&s_xm[sb + 4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xm[e] = lo[e];
+        xm[e + 4] = hi[e];
+      }
+    }
+    prepare_planes<Z>(Tc.D, xm);
 #pragma unroll
     for (int jj = 0; jj < NJ; ++jj) {
       const int j = jg * NJ + jj;
@@ -384,36 +397,38 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   }
 }
 
-// y[m][n] = cast(sum_{s=0..splits-1} partial[s][m][n]) (+ bias): four
-// consecutive columns per thread, the ranges added in order 0, 1, ... with up
-// to 16 loads in flight.
-template <typename DT>
+// y[m][n] = cast(sum_{s=0..splits-1} partial[s][m][n]) (+ bias), four
+// consecutive columns per chunk.  TPC lanes of one wave share a chunk: lane
+// `sub` adds ranges sub, sub + TPC, ... in increasing order (all its loads in
+// flight at once), then the TPC sums are combined by a fixed butterfly, so the
+// result is the same on every run.
+template <typename DT, int TPC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M,
                                                             int N, const uint16_t* __restrict__ bias,
                                                             uint16_t* __restrict__ y) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // index of a 4-column chunk
+  constexpr int BATCH = 16;
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = g / TPC;  // 4-column chunk
+  const int sub = (int)(g % TPC);
   const int64_t total = (int64_t)M * N / 4;
-  if (i >= total) return;
-  const int64_t stride = (int64_t)M * N / 4;
-  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(partial) + i;
+  const bool live = i < total;
+  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(partial) + (live ? i : 0);
   f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 16 <= splits; s += 16) {
-    f32x4_t v[16];
+  for (int s0 = sub; s0 < splits; s0 += TPC * BATCH) {
+    f32x4_t v[BATCH];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = __builtin_nontemporal_load(src + (int64_t)(s + k) * stride);
+    for (int k = 0; k < BATCH; ++k) {
+      const int s = s0 + k * TPC;
+      v[k] = (live && s < splits) ? __builtin_nontemporal_load(src + (int64_t)s * total) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc += v[k];
+    for (int k = 0; k < BATCH; ++k) acc += v[k];
   }
-  if (s < splits) {
-    f32x4_t v[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-      if (s + k < splits) v[k] = __builtin_nontemporal_load(src + (int64_t)(s + k) * stride);
+  for (int o = TPC / 2; o >= 1; o >>= 1)
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-      if (s + k < splits) acc += v[k];
-  }
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  if (!live || sub != 0) return;
   const int n = (int)((i * 4) % N);
   uint16_t o[4];
 #pragma unroll
@@ -505,13 +520,29 @@ int launch_decode(const DecodeParams& p, const DecodePlan& pl, int max_bits, int
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 
-int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream_t st) {
+template <typename DT, int TPC>
+static void launch_reduce_t(const DecodeParams& p, int splits, hipStream_t st) {
   const int64_t chunks = (int64_t)p.M * p.N / 4;
-  const dim3 grid((unsigned)((chunks + 255) / 256));
-  if (dtype == GRINQH_DTYPE_BF16)
-    hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, dim3(256), 0, st, p.partial, splits, p.M, p.N, p.bias, p.y);
+  const dim3 grid((unsigned)((chunks * TPC + 255) / 256));
+  hipLaunchKernelGGL((splitk_reduce_kernel<DT, TPC>), grid, dim3(256), 0, st, p.partial, splits, p.M, p.N, p.bias,
+                     p.y);
+}
+
+template <typename DT>
+static void launch_reduce_dt(const DecodeParams& p, int splits, hipStream_t st) {
+  if (splits >= 64)
+    launch_reduce_t<DT, 16>(p, splits, st);
+  else if (splits >= 8)
+    launch_reduce_t<DT, 4>(p, splits, st);
   else
-    hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, dim3(256), 0, st, p.partial, splits, p.M, p.N, p.bias, p.y);
+    launch_reduce_t<DT, 1>(p, splits, st);
+}
+
+int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream_t st) {
+  if (dtype == GRINQH_DTYPE_BF16)
+    launch_reduce_dt<BF16>(p, splits, st);
+  else
+    launch_reduce_dt<F16>(p, splits, st);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

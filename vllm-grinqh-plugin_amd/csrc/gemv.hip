@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
 
   __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
   __shared__ __align__(16) uint16_t s_bv[RMAX];               // row -> correction-column value
+  __shared__ __align__(16) uint32_t s_xm[RMAX];               // row -> zone-0 flip
   __shared__ __align__(16) uint16_t s_scale[SCG * 16 * 64];   // (group, tile, word column) scales
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
@@ -118,8 +119,9 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   }
   __syncthreads();
 
-  // ---- phase 1b: grade each row: correction-column value and plane offsets (the
-  // code bytes are consumed in offset binary, w_eff * 2^sh = u + beta * 2^sh - 128)
+  // ---- phase 1b: grade each row: correction-column value, zone-0 flip and plane
+  // offsets (w_eff * 2^sh = u + beta * 2^sh - (zone 0 active ? 128 : 0), with u the
+  // offset-binary byte when zone 0 is active, else U & mask)
   for (int rr = tid; rr < R; rr += 256) {
     uint32_t bits;
     if (DENSE) {
@@ -135,7 +137,8 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
       bits = zone_bits<Z>(s, p.thr.t);
     }
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
-    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - 128);
+    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - ((bits & 1u) ? 128 : 0));
+    s_xm[rr] = zone0_flip(bits);
     const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
 #pragma unroll
     for (int z = 0; z < Z; ++z)
@@ -201,7 +204,17 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
 
     const u32x4_t A = *reinterpret_cast<const u32x4_t*>(a_row + 8 * t);
     const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[8 * t]);
-    prepare_planes<Z>(Dc);
+    uint32_t xm[8];
+    {
+      const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&s_xm[8 * t]);
+      const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&s_xm[8 * t + 4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xm[e] = lo[e];
+        xm[e + 4] = hi[e];
+      }
+    }
+    prepare_planes<Z>(Dc, xm);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint32_t V[8];

@@ -148,21 +148,25 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 
 // Code-byte rebuild for 8 rows of plane words D[e][z] (one word per plane).
 // Plane z's digit of slot j sits in field 3-j of each byte (bits 8*beta+6-2j).
-// prepare_planes flips zone 0's top digit bit (offset binary: the byte becomes
-// int8(U & mask) + 128, also for rows whose zone 0 was not loaded) and rotates
+// prepare_planes flips zone 0's top digit bit where zone 0 is active (offset
+// binary: the byte becomes int8(U & mask) + 128) and rotates
 // G_z = rot(D_z, 2z), which moves slot j's digit to field (3-z-j)&3; then
 // code_dwords merges field (3-z-j)&3 of every G_z (the fields are disjoint)
 // and rotates back: V_j = rot(H_j, -2j) holds the code bytes of column tiles
 // 4j+beta, digit z in field 3-z.
+// xm[e] is the zone-0 flip of row e: 0xAAAAAAAA when zone 0 is active (the
+// byte is then int8(U & mask) + 128), 0 otherwise (the byte is U & mask, which
+// has bit 7 clear).  A row with no active zone thus rebuilds to exact zeros.
 template <int Z>
-__device__ __forceinline__ void prepare_planes(uint32_t (&D)[8][Z]) {
+__device__ __forceinline__ void prepare_planes(uint32_t (&D)[8][Z], const uint32_t (&xm)[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    D[e][0] ^= 0xAAAAAAAAu;
+    D[e][0] ^= xm[e];
 #pragma unroll
     for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
   }
 }
+__device__ __forceinline__ uint32_t zone0_flip(uint32_t bits) { return (bits & 1u) ? 0xAAAAAAAAu : 0u; }
 template <int Z>
 __device__ __forceinline__ void code_dwords(const uint32_t (&G)[8][Z], int j, uint32_t (&V)[8]) {
 #pragma unroll
