@@ -308,7 +308,7 @@ def test_split_k_is_deterministic():
         assert torch.equal(grinqh_gemv_batch_union(xt, P, st, None, 8, 128, 1024, t), y0)
 
 
-@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("M", [1, 3, 20])
 def test_nonfinite_rows_poison_their_output_row(M):
     """A NaN or inf activation makes its whole output row NaN, as the
     reference's sum of beta*x (0*NaN, 0*inf) does (grinqh/kernel.py:113-114)."""

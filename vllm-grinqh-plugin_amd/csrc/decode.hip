@@ -437,14 +437,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                    (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
 }
 
-// sigma_k = max_m |x[m][k]| over the whole batch (NaN ignored unless all NaN),
-// for launches that split a batch into several decode calls.
+// sigma_k = max_m |x[m][k]| over the whole batch (NaN ignored unless all NaN,
+// as fmaxf does), computed once for kernels that grade from it.  A block
+// covers 32 columns; its 8 row groups take every 8th row with 8 loads in
+// flight each, and the 8 partial maxima are combined through LDS.
 template <typename DT>
 __global__ __launch_bounds__(256) void sigma_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                                                     float* __restrict__ sigma) {
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= K) return;
-  sigma[k] = column_absmax<DT>(x, ldx, M, k);
+  constexpr int COLS = 32, GROUPS = 256 / COLS, BATCH = 8;
+  __shared__ float s_part[GROUPS][COLS];
+  const int kk = threadIdx.x % COLS, mg = threadIdx.x / COLS;
+  const int k = blockIdx.x * COLS + kk;
+  const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
+  float s = __int_as_float(0x7fc00000);  // NaN: no row seen yet
+  for (int m0 = mg; m0 < M; m0 += GROUPS * BATCH) {
+    uint16_t v[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const int m = min(m0 + GROUPS * i, M - 1);  // rows past the end repeat the last row
+      v[i] = x[(int64_t)m * ldx + kc];
+    }
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) s = fmaxf(s, fabsf(to_f32<DT>(v[i])));
+  }
+  s_part[mg][kk] = s;
+  __syncthreads();
+  if (mg == 0 && k < K) {
+#pragma unroll
+    for (int g = 1; g < GROUPS; ++g) s = fmaxf(s, s_part[g][kk]);
+    sigma[k] = s;
+  }
 }
 
 DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
@@ -548,7 +570,7 @@ int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream
 
 int launch_sigma(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* sigma, hipStream_t st) {
   if (K == 0) return GRINQH_OK;
-  const dim3 grid((K + 255) / 256);
+  const dim3 grid((K + 31) / 32);
   if (dtype == GRINQH_DTYPE_BF16)
     hipLaunchKernelGGL(sigma_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, sigma);
   else
