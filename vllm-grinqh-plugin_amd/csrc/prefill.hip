@@ -65,8 +65,8 @@ struct Dequant<BF16, SH> {
 // loads are issued before the previous stage's MFMAs and consumed after them,
 // so a longer stage hides more load latency.  Each dequantizing thread owns one
 // word column, BK/16 rows and 4*JPT column tiles.
-template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK>
-__global__ __launch_bounds__(WAVES * 64, 1) void prefill_kernel(PrefillParams p) {
+template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC>
+__global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int SH = 8 - 2 * Z;
   constexpr int KP = BK + 8;        // halves per LDS row (padding: conflict-free fragment reads)
@@ -258,22 +258,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void prefill_kernel(PrefillParams p)
     }
 }
 
-template <typename DT, int BM, int Z, int WAVES, int BK>
+template <typename DT, int BM, int Z, int WAVES, int BK, int OCC>
 static void launch_prefill_t(const PrefillParams& p, bool dense, hipStream_t st) {
   const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM);
   if (dense)
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK>), grid, dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK, OCC>), grid, dim3(WAVES * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK>), grid, dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK, OCC>), grid, dim3(WAVES * 64), 0, st, p);
 }
 
-template <typename DT, int BM, int WAVES, int BK>
+template <typename DT, int BM, int WAVES, int BK, int OCC = 1>
 static int launch_prefill_bm(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
   switch (Z) {
-    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK>(p, dense, st); break;
-    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK>(p, dense, st); break;
-    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK>(p, dense, st); break;
-    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK>(p, dense, st); break;
+    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK, OCC>(p, dense, st); break;
+    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK, OCC>(p, dense, st); break;
+    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK, OCC>(p, dense, st); break;
+    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK, OCC>(p, dense, st); break;
     default: return GRINQH_ERR_INVALID;
   }
   return GRINQH_OK;
