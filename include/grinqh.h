@@ -84,10 +84,12 @@ int grinqh_dequantize(const void* planes_u32, const void* scale, void* out, int6
 int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, int max_bits,
                  const float thresholds[4], uint8_t* zone_bits, int32_t* beta, void* stream);
 
-/* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none): fp32
- * split-K partial sums and, for union batches of more than 64 rows, the
- * per-row grading statistic.  No initial contents are required.  Calls that
- * share a workspace must be ordered (same stream); it must be 256-byte aligned. */
+/* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none): split-K
+ * completion counters, fp32 split-K partial sums and, for union batches of
+ * more than 16 rows, the per-row grading statistic.  It must be zero-filled
+ * once before its first use (every call leaves its counters zero again; the
+ * rest needs no initial contents), 256-byte aligned, and calls that share it
+ * must be ordered (same stream). */
 size_t grinqh_workspace_bytes(int64_t M, int64_t K, int64_t N, int max_bits, int mode);
 
 /* The quantized linear y[M][N] = x[M][K] * W_eff (+ bias), x/scale/bias/y in `dtype`.

@@ -308,6 +308,32 @@ def test_split_k_is_deterministic():
         assert torch.equal(grinqh_gemv_batch_union(xt, P, st, None, 8, 128, 1024, t), y0)
 
 
+def test_split_k_counters_return_to_zero():
+    """Where a column block's partial sums are small (at most 64 KiB), the K
+    range that finishes last completes split-K inside the main kernel and
+    clears its column block's counter: after every call the workspace's
+    counter area (its first 16 KiB) is zero again, so calls of any shape share
+    one workspace.  Larger reductions and column counts that are not a
+    multiple of 64 take the separate reduction kernel; both paths match the
+    oracle."""
+    from grinqh.kernel import _WORKSPACES, grinqh_gemv_batch_union
+    rng = np.random.default_rng(9)
+    t = [0.0, 0.5, 1.0, 2.0]
+    dev = torch.device("cuda", 0)
+    for M, K, N in [(1, 1024, 16384), (4, 256, 16384), (16, 1024, 16384), (2, 512, 8192),  # in the kernel
+                    (1, 4096, 6144), (4, 4096, 4096), (64, 4096, 1024), (1, 4096, 32), (20, 1024, 96)]:
+        W, x, s = _setup(rng, K, N, 8, "float16", M=M, scale_sd=0.01)
+        xt, P, st = _tdt(x, "float16"), _prepare(W, 8), _tdt(s, "float16")
+        y = grinqh_gemv_batch_union(xt, P, st, None, 8, 128, N // 4, t)
+        torch.cuda.synchronize()
+        ws = _WORKSPACES.get(dev, torch.cuda.current_stream(dev).cuda_stream, 1)
+        assert ws is not None and int(ws[:16384].count_nonzero()) == 0, f"counters left set after M={M} K={K} N={N}"
+        assert torch.equal(grinqh_gemv_batch_union(xt, P, st, None, 8, 128, N // 4, t), y)
+        pre = O.gemv_union_f64(x, W, s, t, 8, 128)
+        assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, 8, 128, "float16"), "float16",
+                            what=f"M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M", [1, 3, 20])
 def test_nonfinite_rows_poison_their_output_row(M):
     """A NaN or inf activation makes its whole output row NaN, as the

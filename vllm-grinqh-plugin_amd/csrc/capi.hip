@@ -30,7 +30,7 @@ struct KernelEvents {
 KernelEvents g_events;
 
 struct WorkspaceLayout {
-  size_t sigma_off, partial_off, total;
+  size_t counter_off, sigma_off, partial_off, total;
   DecodePlan plan;
 };
 
@@ -45,7 +45,10 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
                              : launch_decode(p, plan, max_bits, dtype, dense, st);
 }
 
-// [sigma (K floats, union batches split into several launches) | split-K partials]
+// [split-K counters (kCounterBytes, zero between calls) | sigma (K floats,
+// graded batches above kSigmaPrepassRows) | split-K partials].  The counters
+// sit at offset 0 for every shape, so a workspace shared by calls of different
+// shapes keeps them zero.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   size_t partial = 0;
@@ -54,7 +57,8 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
     partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   }
   const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kSigmaPrepassRows;
-  w.sigma_off = 0;
+  w.counter_off = 0;
+  w.sigma_off = kCounterBytes;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
   return w;
@@ -160,6 +164,9 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
     p.M = (int)mc;
     p.splits = plan.splits;
     p.tiles_per_split = plan.tiles_per_split;
+    const int64_t block_cols = mc <= kGemvMaxRows ? 1024 : 256;  // logical columns per column block
+    p.counters =
+        splitk_in_kernel(plan, mc, N, block_cols) ? reinterpret_cast<uint32_t*>(ws + wl.counter_off) : nullptr;
     hipEvent_t ev_after = nullptr;
     if (m0 == 0) {
       std::lock_guard<std::mutex> lock(g_events.mu);
@@ -172,7 +179,7 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
     rc = launch_main(p, plan, max_bits, dtype, !graded, st);
     if (rc != GRINQH_OK) return rc;
     if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
-    if (plan.splits > 1) {
+    if (plan.splits > 1 && p.counters == nullptr) {
       rc = launch_splitk_reduce(p, plan.splits, dtype, st);
       if (rc != GRINQH_OK) return rc;
     }

@@ -7,9 +7,11 @@
 // small batches (:663-680, semantics of :561-587).
 //
 // Work decomposition
-//   grid.x  = column block: 16 plane-word columns w0..w0+15 = 256 logical
-//             columns (16 column tiles r of 16 contiguous columns r*NW + w0 + c)
-//   grid.y  = K range of `tiles_per_split` 32-row tiles (split-K)
+//   block   = (column block, K range), one-dimensional grid renumbered per XCD
+//   column block: 16 plane-word columns w0..w0+15 = 256 logical columns (16
+//             column tiles r of 16 contiguous columns r*NW + w0 + c); two
+//             neighbours share every 128-byte line of the planes
+//   K range = `tiles_per_split` 32-row tiles (split-K)
 //   4 waves = MT groups of output dwords j x (4/MT) K sub-ranges
 //
 // Phase 1 (whole block): stage x[:, K range] in LDS, grade every row (sigma =
@@ -37,6 +39,7 @@
 // adds the fp32 partials in range order and applies the output cast and bias.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
+#include "splitk_complete.h"
 
 namespace grinqh {
 
@@ -77,8 +80,12 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int jg = wave % MT, kw = wave / MT;
   const int c = lane & 15, q = lane >> 4;
-  const int w0 = blockIdx.x * 16;
-  const int split = blockIdx.y;
+  // logical block = (column block, K range), column blocks fastest, ranges of
+  // consecutive logical blocks per XCD (adjacent column blocks share lines)
+  const int col_blocks = (p.NW + 15) >> 4;
+  const int lb = xcd_chunked(blockIdx.x, gridDim.x);
+  const int w0 = (lb % col_blocks) * 16;
+  const int split = lb / col_blocks;
   const int ntiles_total = p.K >> 5;
   const int tile0 = split * p.tiles_per_split;
   const int tile1 = min(tile0 + p.tiles_per_split, ntiles_total);
@@ -380,7 +387,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   }
 
   // Split-K: this K range's partial sums go to partial[split][m][n]; the
-  // reduce kernel that follows on the stream adds the ranges in fixed order.
+  // range that finishes last (or the reduce kernel that follows on the
+  // stream) adds the ranges in fixed order.
   if (kw == 0 && col_ok) {
     float* part = p.partial + (int64_t)split * p.M * p.N;
 #pragma unroll
@@ -392,9 +400,10 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int m = 16 * mt + 4 * q + e;
-            if (m < p.M) part[(int64_t)m * p.N + col_of(jj, b)] = Y[mt][jj][b][e];
+            if (m < p.M) store_partial(&part[(int64_t)m * p.N + col_of(jj, b)], Y[mt][jj][b][e]);
           }
   }
+  if (p.counters != nullptr) splitk_complete<DT, 4 * MT>(p, lb % col_blocks, w0, 16);
 }
 
 // y[m][n] = cast(sum_{s=0..splits-1} partial[s][m][n]) (+ bias), four
@@ -504,7 +513,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
 
 template <typename DT, int MT, int Z>
 static void launch_decode_t(const DecodeParams& p, const DecodePlan& pl, bool dense, hipStream_t st) {
-  const dim3 grid(pl.col_blocks, pl.splits);
+  const dim3 grid(pl.col_blocks * pl.splits);
   if (dense)
     hipLaunchKernelGGL((decode_kernel<DT, MT, Z, true>), grid, dim3(256), 0, st, p);
   else

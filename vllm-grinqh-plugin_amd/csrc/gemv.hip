@@ -23,18 +23,43 @@
 //   through LDS in fixed order; K ranges are reduced by the split-K kernel.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
+#include "splitk_complete.h"
 
 namespace grinqh {
 
 constexpr int kGemvRowsPerBlock = 1024;   // rows of x staged per block
 constexpr int kGemvScaleGroups = 9;       // scale groups staged per block
-// One row (MR = 1) fits two resident blocks per CU (256 registers per lane);
-// up to four rows (MR = 4) keep one block per CU.
-constexpr int gemv_blocks_per_cu(int mr) { return mr == 1 ? 2 : 1; }
+// Two resident blocks per CU (256 registers per lane) for one row on 8-row
+// tiles and for up to four rows on 4-row tiles.
+constexpr int gemv_tile_rows(int mr) { return mr == 1 ? 8 : 4; }
+constexpr int gemv_blocks_per_cu(int) { return 2; }
+
+// Tiles of TR rows: 8 rows on v_mfma_f32_16x16x32 (one x row), 4 rows on
+// v_mfma_f32_16x16x16 (up to four x rows: half the plane words in flight per
+// tile, which leaves room for the 64 accumulators at two blocks per CU).
+template <int TR>
+struct GemvTile;
+template <>
+struct GemvTile<8> {
+  typedef u32x4_t vec_t;
+};
+template <>
+struct GemvTile<4> {
+  typedef u32x2_t vec_t;
+};
+template <typename DT, int TR>
+__device__ __forceinline__ f32x4_t tile_mfma(const typename GemvTile<TR>::vec_t& a,
+                                             const typename GemvTile<TR>::vec_t& b, f32x4_t c) {
+  if constexpr (TR == 8)
+    return mfma16x16x32<DT>(a, b, c);
+  else
+    return mfma16x16x16<DT>(a, b, c);
+}
 
 template <typename DT, int MR, int Z, bool DENSE>
 __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(DecodeParams p) {
   constexpr int SH = 8 - 2 * Z;
+  constexpr int TR = gemv_tile_rows(MR);
   constexpr int RMAX = kGemvRowsPerBlock;
   constexpr int XS = RMAX + 8;                 // halves per staged x row
   constexpr int X_BYTES = 5 * XS * 2;          // x rows 0..3, row 4 all zero
@@ -146,7 +171,8 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   }
   __syncthreads();
 
-  // ---- phase 2: this wave's 8-row tiles
+  // ---- phase 2: this wave's TR-row tiles
+  typedef typename GemvTile<TR>::vec_t vec_t;
   f32x4_t C[4][4];
   f32x4_t Cv;
   float Y[4][4][MR];
@@ -158,8 +184,8 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
       for (int i = 0; i < MR; ++i) Y[j][b][i] = 0.f;
 
   const float post = BOperand<DT>::kUnit / (float)(1 << SH);
-  const int n8 = R >> 3;
-  const int t_begin = (n8 * wave) >> 2, t_end = (n8 * (wave + 1)) >> 2;
+  const int nt = R / TR;
+  const int t_begin = (nt * wave) >> 2, t_end = (nt * (wave + 1)) >> 2;
   // A operand rows: lane (c, q) carries x row c & 3 when c >> 2 == q, else the zero row
   const uint16_t* a_row = s_x + (((c >> 2) == q) ? (c & 3) : 4) * XS;
 
@@ -175,12 +201,12 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   const uint32_t lane_off = (uint32_t)wc * 4u;
 
   typedef uint32_t offz_t __attribute__((ext_vector_type(Z)));
-  auto issue = [&](int t, uint32_t (&D)[8][Z]) {
+  auto issue = [&](int t, uint32_t (&D)[TR][Z]) {
     const bool live = t < t_end;
     const __amdgpu_buffer_rsrc_t rs = live ? prsrc : prsrc_none;
-    const int sb = (live ? t : t_begin) * 8;
+    const int sb = (live ? t : t_begin) * TR;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < TR; ++e) {
       offz_t o;
       if constexpr (Z == 1) {
         o = s_off[sb + e];
@@ -195,41 +221,41 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     }
   };
 
-  auto step = [&](int t, uint32_t (&Dc)[8][Z], bool prefetch, uint32_t (&Dn)[8][Z]) {
-    const int rowa = row0 + 8 * t;
+  auto step = [&](int t, uint32_t (&Dc)[TR][Z], bool prefetch, uint32_t (&Dn)[TR][Z]) {
+    const int rowa = row0 + TR * t;
     const bool first_of_group = (t == t_begin) || (rowa % p.gs == 0);
-    const bool last_of_group = (t + 1 == t_end) || ((rowa + 8) % p.gs == 0);
+    const bool last_of_group = (t + 1 == t_end) || ((rowa + TR) % p.gs == 0);
     if (prefetch) issue(t + 2, Dn);
     __builtin_amdgcn_sched_barrier(0);
 
-    const u32x4_t A = *reinterpret_cast<const u32x4_t*>(a_row + 8 * t);
-    const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[8 * t]);
-    uint32_t xm[8];
-    {
-      const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(&s_xm[8 * t]);
-      const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(&s_xm[8 * t + 4]);
+    const vec_t A = *reinterpret_cast<const vec_t*>(a_row + TR * t);
+    const vec_t bv = *reinterpret_cast<const vec_t*>(&s_bv[TR * t]);
+    uint32_t xm[TR];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xm[e] = lo[e];
-        xm[e + 4] = hi[e];
-      }
+    for (int h = 0; h < TR / 4; ++h) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&s_xm[TR * t + 4 * h]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xm[4 * h + e] = v[e];
     }
-    prepare_planes<Z>(Dc, xm);
+    prepare_planes<Z, TR>(Dc, xm);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t V[8];
-      code_dwords<Z>(Dc, j, V);
-      u32x4_t B[4];
-      BOperand<DT>::build(V, B);
+      uint32_t V[TR];
+      code_dwords<Z, TR>(Dc, j, V);
+      vec_t B[4];
+#pragma unroll
+      for (int pr = 0; pr < TR / 2; ++pr)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) B[b][pr] = BOperand<DT>::pair(V[2 * pr], V[2 * pr + 1], b);
       if (first_of_group) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) C[j][b] = mfma16x16x32<DT>(A, B[b], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        for (int b = 0; b < 4; ++b) C[j][b] = tile_mfma<DT, TR>(A, B[b], f32x4_t{0.f, 0.f, 0.f, 0.f});
       } else {
 #pragma unroll
-        for (int b = 0; b < 4; ++b) C[j][b] = mfma16x16x32<DT>(A, B[b], C[j][b]);
+        for (int b = 0; b < 4; ++b) C[j][b] = tile_mfma<DT, TR>(A, B[b], C[j][b]);
       }
     }
-    Cv = mfma16x16x32<DT>(A, bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv);
+    Cv = tile_mfma<DT, TR>(A, bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv);
 
     if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv)
       const uint16_t* srow = &s_scale[(rowa / p.gs - g_first) * 1024 + lane];
@@ -245,7 +271,7 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   };
 
   {
-    uint32_t DA[8][Z], DB[8][Z], DC[8][Z];
+    uint32_t DA[TR][Z], DB[TR][Z], DC[TR][Z];
     issue(t_begin, DA);
     issue(t_begin + 1, DB);
     int t = t_begin;
@@ -269,32 +295,36 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
         for (int i = 0; i < MR; ++i) s_red[((wave - 1) * 16 * MR + (4 * j + b) * MR + i) * 64 + lane] = Y[j][b][i];
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave == 0) {
+#pragma unroll 1
+    for (int k = 0; k < 3; ++k)
 #pragma unroll
-  for (int k = 0; k < 3; ++k)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+        for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int i = 0; i < MR; ++i) Y[j][b][i] += s_red[(k * 16 * MR + (4 * j + b) * MR + i) * 64 + lane];
+          for (int i = 0; i < MR; ++i) Y[j][b][i] += s_red[(k * 16 * MR + (4 * j + b) * MR + i) * 64 + lane];
 
-  // ---- phase 4: output column n = (4j + b) * NW + w of rows m < M
-  if (!col_ok) return;
+    // ---- phase 4: output column n = (4j + b) * NW + w of rows m < M
+    if (col_ok) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int64_t n = (int64_t)(4 * j + b) * p.NW + wc;
+        for (int b = 0; b < 4; ++b) {
+          const int64_t n = (int64_t)(4 * j + b) * p.NW + wc;
 #pragma unroll
-      for (int i = 0; i < MR; ++i) {
-        if (i >= p.M) break;
-        if (p.splits == 1)
-          p.y[(int64_t)i * p.N + n] = finish_output<DT>(Y[j][b][i], p.bias, (int)n);
-        else
-          p.partial[((int64_t)split * p.M + i) * p.N + n] = Y[j][b][i];
-      }
+          for (int i = 0; i < MR; ++i) {
+            if (i >= p.M) break;
+            if (p.splits == 1)
+              p.y[(int64_t)i * p.N + n] = finish_output<DT>(Y[j][b][i], p.bias, (int)n);
+            else
+              store_partial(&p.partial[((int64_t)split * p.M + i) * p.N + n], Y[j][b][i]);
+          }
+        }
     }
+  }
+  // the K range that finishes last adds all ranges' partial sums of this column block
+  if (p.splits > 1 && p.counters != nullptr) splitk_complete<DT, MR>(p, blockIdx.x, w0, 64);
 }
 
 // The plan sizes K ranges for a group size of 32 (the largest split count);

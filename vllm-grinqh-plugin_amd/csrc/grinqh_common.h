@@ -91,6 +91,38 @@ __device__ __forceinline__ f32x4_t mfma16x16x32<BF16>(const u32x4_t& a, const u3
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x16_{f16,bf16}: lane (c, q) holds A[c][4q..4q+3] and
+// B[4q..4q+3][c]; D as for 16x16x32.
+template <typename DT>
+__device__ __forceinline__ f32x4_t mfma16x16x16(const u32x2_t& a, const u32x2_t& b, f32x4_t c);
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x16<F16>(const u32x2_t& a, const u32x2_t& b, f32x4_t c) {
+  typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(half4_t, a), __builtin_bit_cast(half4_t, b), c,
+                                               0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4_t mfma16x16x16<BF16>(const u32x2_t& a, const u32x2_t& b, f32x4_t c) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, a), __builtin_bit_cast(short4_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- block order
+
+// The workgroups of a launch are dealt to the 8 XCDs round robin (linear id
+// mod 8), and each XCD has its own L2.  xcd_chunked renumbers linear id L of
+// `total` workgroups so that every XCD runs one contiguous range of logical
+// blocks: logical neighbours (column blocks that share 128-byte lines) meet in
+// one L2 instead of each XCD fetching the whole line.  A bijection on
+// [0, total) for any total.
+__device__ __forceinline__ int xcd_chunked(int L, int total) {
+  constexpr int kXcds = 8;
+  const int per = total / kXcds, rem = total % kXcds;
+  const int xcd = L % kXcds, slot = L / kXcds;
+  return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
 // ---------------------------------------------------------------- grading
 
 // sigma_k = max_m |x[m][k]| with NaN ignored (fmaxf) unless every entry is NaN.
@@ -157,20 +189,20 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
 // xm[e] is the zone-0 flip of row e: 0xAAAAAAAA when zone 0 is active (the
 // byte is then int8(U & mask) + 128), 0 otherwise (the byte is U & mask, which
 // has bit 7 clear).  A row with no active zone thus rebuilds to exact zeros.
-template <int Z>
-__device__ __forceinline__ void prepare_planes(uint32_t (&D)[8][Z], const uint32_t (&xm)[8]) {
+template <int Z, int E = 8>
+__device__ __forceinline__ void prepare_planes(uint32_t (&D)[E][Z], const uint32_t (&xm)[E]) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < E; ++e) {
     D[e][0] ^= xm[e];
 #pragma unroll
     for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
   }
 }
 __device__ __forceinline__ uint32_t zone0_flip(uint32_t bits) { return (bits & 1u) ? 0xAAAAAAAAu : 0u; }
-template <int Z>
-__device__ __forceinline__ void code_dwords(const uint32_t (&G)[8][Z], int j, uint32_t (&V)[8]) {
+template <int Z, int E = 8>
+__device__ __forceinline__ void code_dwords(const uint32_t (&G)[E][Z], int j, uint32_t (&V)[E]) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < E; ++e) {
     // with all four planes the last one fills the remaining field, otherwise
     // the fields no plane owns are zero
     uint32_t h = (Z == 4) ? G[e][3] : (G[e][0] & (0x03030303u << (2 * ((3 - j) & 3))));
@@ -198,8 +230,11 @@ struct BOperand<F16> {
 #pragma unroll
     for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int beta = 0; beta < 4; ++beta)
-        B[beta][p] = perm(V[2 * p + 1], V[2 * p], 0x0C040C00u + (uint32_t)beta * 0x00010001u);
+      for (int beta = 0; beta < 4; ++beta) B[beta][p] = pair(V[2 * p], V[2 * p + 1], beta);
+  }
+  // rows e0 (low half) and e1 (high half) of column tile beta
+  __device__ __forceinline__ static uint32_t pair(uint32_t v0, uint32_t v1, int beta) {
+    return perm(v1, v0, 0x0C040C00u + (uint32_t)beta * 0x00010001u);
   }
   __device__ __forceinline__ static uint16_t correction(int v) {  // v * 2^-24, |v| < 1024
     return v >= 0 ? (uint16_t)v : (uint16_t)(0x8000u | (uint32_t)(-v));
@@ -212,14 +247,14 @@ struct BOperand<BF16> {
   static constexpr float kUnit = 1.f;
   __device__ __forceinline__ static void build(const uint32_t (&V)[8], u32x4_t (&B)[4]) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int beta = 0; beta < 4; ++beta) {
-        const float a = (float)((V[2 * p] >> (8 * beta)) & 0xFFu);
-        const float b = (float)((V[2 * p + 1] >> (8 * beta)) & 0xFFu);
-        B[beta][p] = perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
-      }
-    }
+      for (int beta = 0; beta < 4; ++beta) B[beta][p] = pair(V[2 * p], V[2 * p + 1], beta);
+  }
+  __device__ __forceinline__ static uint32_t pair(uint32_t v0, uint32_t v1, int beta) {
+    const float a = (float)((v0 >> (8 * beta)) & 0xFFu);
+    const float b = (float)((v1 >> (8 * beta)) & 0xFFu);
+    return perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
   }
   __device__ __forceinline__ static uint16_t correction(int v) { return from_f32<BF16>((float)v); }
 };

@@ -28,6 +28,8 @@ struct DecodeParams {
   int tiles_per_split;  // 32-row tiles per K range
   float* partial;       // [splits][M][N] fp32 when splits > 1
   const float* sigma;   // optional precomputed union statistic [K] (else computed from x)
+  uint32_t* counters;   // per column block, zero on entry: the kernel completes split-K
+                        // itself; nullptr: partial sums only, the reduce kernel follows
 };
 
 struct DecodePlan {
@@ -40,7 +42,24 @@ struct DecodePlan {
 
 DecodePlan plan_decode(int64_t M, int64_t K, int64_t N);
 
-// Main kernels only: when plan.splits > 1 the caller follows with launch_splitk_reduce.
+// Split-K completion counters (one per column block) at the start of the
+// workspace; larger column counts fall back to the reduce kernel.
+constexpr int64_t kMaxCounters = 4096;
+constexpr size_t kCounterBytes = size_t(kMaxCounters) * 4;
+// Partial-sum bytes one column block's last K range may add up itself; above
+// this one block's reads would outlast a separate, grid-wide reduction.
+constexpr int64_t kInKernelReduceBytes = 64 << 10;
+// Whether the main kernel completes split-K itself (DecodeParams::counters):
+// whole 4-column chunks per column block, 32-bit partial-sum offsets and a
+// small enough reduction.  cols = logical columns per column block.
+inline bool splitk_in_kernel(const DecodePlan& pl, int64_t M, int64_t N, int64_t cols) {
+  return pl.splits > 1 && (N / 16) % 4 == 0 && pl.col_blocks <= kMaxCounters &&
+         (int64_t)pl.splits * M * N * 4 < ((int64_t)1 << 31) &&
+         (int64_t)pl.splits * M * cols * 4 <= kInKernelReduceBytes;
+}
+
+// Main kernels: when plan.splits > 1 and p.counters is null the caller
+// follows with launch_splitk_reduce.
 int launch_decode(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense,
                   hipStream_t st);
 // y = cast(sum over `splits` of partial[s][M][N]) (+ bias), ranges added in order

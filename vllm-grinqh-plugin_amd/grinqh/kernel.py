@@ -40,10 +40,11 @@ def batch_grading_mode() -> str:
 
 
 class _Workspaces:
-    """Per (device, stream) scratch for split-K partial sums.
+    """Per (device, stream) workspace: split-K counters and partial sums.
 
-    Grown on demand (no initial contents are needed).  Calls on one stream are
-    ordered, so they may share it; different streams get different buffers."""
+    Grown on demand and zero-filled when allocated (the library keeps its
+    counters zero between calls).  Calls on one stream are ordered, so they
+    may share it; different streams get different buffers."""
 
     def __init__(self):
         self._bufs = {}
@@ -61,7 +62,7 @@ class _Workspaces:
                         "GRINQH: workspace must be allocated before graph capture; run the largest "
                         "batch once eagerly first")
                 size = max(nbytes, 1 << 20)
-                buf = torch.empty(size, dtype=torch.uint8, device=device)
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
