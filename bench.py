@@ -12,8 +12,10 @@ exceed 2x the 256 MB MALL, so timings reflect HBM.
 value = whole-step HBM throughput in algorithmic bytes (planes actually needed
 by the grading + scales + x + y) per second.  The JSON line also carries the
 per-case kernel times, the roofline of the dominant kernel, the prefill
-TFLOP/s at M=2048 (BASELINE configs[2] shapes, dense) and the CPU baseline
-(the reference's pure-PyTorch math on the host cores).
+TFLOP/s at M=2048 (dense, the reference's dispatch for M > 1), the graded
+prefill sweep of BASELINE configs[2] (M = 512, 2048, 8192, 70/20/8/2 % grade
+mix) and the CPU baseline (the reference's pure-PyTorch math on the host
+cores).
 """
 from __future__ import annotations
 
@@ -37,6 +39,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 SHAPES = [("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 28672), ("down", 14336, 4096)]
 DECODE_M = [1, 4, 16, 64]
 PREFILL_M = 2048
+PREFILL_GRADED_M = (512, 2048, 8192)
 GS = 128
 BITS = 8
 MALL_BYTES = 256 << 20
@@ -294,6 +297,33 @@ def main() -> int:
                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
             log(f"prefill {name:8s} M={PREFILL_M} {us:9.1f} us {tf:7.1f} TFLOP/s")
 
+    # ---------------- graded prefill sweep: union grading with the
+    # 70/20/8/2% grade mix (t = [0, P70, P90, P98] of the batch statistic)
+    prefill_graded = None
+    if not args.no_prefill:
+        prefill_graded = []
+        for i, (name, K, N) in enumerate(SHAPES):
+            for M in PREFILL_GRADED_M:
+                x = synth_x(torch, M, K, 199 + i, dev)
+                t = thresholds_for(x, (0.7, 0.9, 0.98))
+                p, s = copies[name][0]
+                with torch.cuda.stream(stream):
+                    run_product(x, p, s, None, BITS, GS, N // 4, t, "union")
+                    torch.cuda.synchronize()
+                    e0.record(stream)
+                    n_it = 3
+                    for j in range(n_it):
+                        pj, sj = copies[name][j % n_copies]
+                        run_product(x, pj, sj, None, BITS, GS, N // 4, t, "union")
+                    e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / n_it
+                tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
+                prefill_graded.append({"shape": name, "M": M, "us": round(us, 2), "tflops": round(tf, 1),
+                                       "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+                log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
+                del x
+
     # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores
     cpu = None
     if not args.no_cpu_baseline:
@@ -332,6 +362,7 @@ def main() -> int:
         "cases": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in c.items() if k not in ("x", "t")}
                   for c in cases],
         "prefill": prefill,
+        "prefill_graded": prefill_graded,
     }
     print(json.dumps(out), flush=True)
     return 0

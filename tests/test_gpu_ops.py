@@ -244,6 +244,34 @@ def test_prefill_dense_shapes(M, K, N, max_bits, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("graded", [False, True])
+def test_prefill_split_k(graded, dtype):
+    """A prefill grid smaller than the GPU (one column block, one row tile) is
+    split into K ranges of whole 32-row stages (K = 65 stages, a last scale
+    group of 32 rows, uneven last range) whose fp32 partial sums are added in
+    order by the reduce kernel, with the bias."""
+    from grinqh.kernel import run_product
+    M, K, N, b = 100, 2080, 256, 8
+    rng = np.random.default_rng(123 + graded)
+    W, x, s = _setup(rng, K, N, b, dtype, M=M)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    if graded:
+        sigma = np.abs(x).max(0).astype(np.float32)
+        t = [0.0] + np.quantile(sigma, [0.7, 0.9, 0.98]).tolist()
+        y = run_product(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128, N // 4, t, "union")
+        pre = O.gemv_union_f64(x, W, s, t, b, 128)
+        fin = O.gemv_union(x, W, s, bias, t, b, 128, dtype)
+        extra = graded_rounding_bound(x, W, s, t, b, dtype)
+    else:
+        y = run_product(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128, N // 4,
+                        [0.0] * 4, "dense")
+        pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+        fin = O.dense_prefill(x, W, s, bias, 128, dtype)
+        extra = dense_rounding_bound(x, W, s, dtype)
+    assert_output_close(y, pre, fin, dtype, bias=bias, what=f"split-K prefill graded={graded}", extra_tol=extra)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_256_row_tiles(dtype):
     """Enough blocks for the 256-row tile variant (64 column blocks x 4 row tiles)."""
     from grinqh.kernel import grinqh_prefill_dense

@@ -52,9 +52,12 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   size_t partial = 0;
-  if (M <= kDecodeMaxRows) {  // larger batches run the prefill kernel, which needs no partial sums
+  if (M <= kDecodeMaxRows) {
     w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
     partial = w.plan.splits > 1 ? w.plan.workspace : 0;
+  } else {  // prefill: partial sums only when its grid is split over K
+    const int splits = prefill_splits(M, K, N);
+    partial = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
   }
   const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kSigmaPrepassRows;
   w.counter_off = 0;
@@ -96,6 +99,8 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   p.NW = d.NW;
   p.gs = d.gs;
   p.sigma = nullptr;
+  p.splits = prefill_splits(M, d.K, d.N);
+  p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
   if (graded) {
     float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
     const int rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
@@ -111,10 +116,18 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
       g_events.before = g_events.after = nullptr;
     }
   }
-  const int rc = launch_prefill(p, max_bits, dtype, !graded, st);
+  int splits_run = 1;
+  int rc = launch_prefill(p, max_bits, dtype, !graded, st, &splits_run);
   if (rc != GRINQH_OK) return rc;
   if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
-  return GRINQH_OK;
+  if (splits_run > 1) {  // add the K ranges in order, cast, bias
+    DecodeParams r = d;
+    r.M = (int)M;
+    r.y = ys;
+    r.partial = p.partial;
+    rc = launch_splitk_reduce(r, splits_run, dtype, st);
+  }
+  return rc;
 }
 
 int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, const void* planes,

@@ -84,11 +84,23 @@ struct PrefillParams {
   GradeThresholds thr;
   int M, K, N, NW, gs;
   const float* sigma;  // union statistic [K] (graded mode), else nullptr
+  int splits;            // grid.z: K ranges (1: y written directly)
+  int stages_per_split;  // set by launch_prefill
+  float* partial;        // [splits][M][N] fp32 when splits > 1 (the reduce kernel follows)
 };
 
-// Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.
-int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st);
+// Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.  p.splits
+// is an upper bound; *splits_run receives the number of K ranges launched
+// (partial sums to reduce when above 1).
+int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st,
+                   int* splits_run);
 int prefill_block_rows(int64_t M, int64_t N);
+// K ranges of a prefill launch: enough to give every CU a block when the
+// (column block, row block) grid alone is smaller, each range at least 256
+// rows of K and the partial sums at most kMaxPrefillPartialBytes.  Depends
+// only on (M, K, N), so the workspace size does too.
+constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
+int prefill_splits(int64_t M, int64_t K, int64_t N);
 
 int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
 int launch_prepare_weight(const int8_t* W, uint32_t* out, int K, int N, int max_bits, hipStream_t st);

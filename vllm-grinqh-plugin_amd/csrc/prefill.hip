@@ -88,7 +88,10 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   const int c = lane & 15, q = lane >> 4;
   const int w0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * BM;
-  const int nstages = p.K / BK;
+  // this block's K range: stages [s_begin, s_end) of BK rows
+  const int nstages_all = p.K / BK;
+  const int s_begin = blockIdx.z * p.stages_per_split;  // < nstages_all: no empty range is launched
+  const int s_end = min(s_begin + p.stages_per_split, nstages_all);
 
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
@@ -106,7 +109,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   bool new_group = false;
   auto load_stage = [&](int s) {
     const int k0 = s * BK;
-    new_group = (s == 0) || (k0 / p.gs != (k0 - BK) / p.gs);
+    new_group = (s == s_begin) || (k0 / p.gs != (k0 - BK) / p.gs);
     if (new_group) {  // this thread's columns: column tiles 4*j0 .., word column wc_ld
       const int g = k0 / p.gs;
 #pragma unroll
@@ -210,12 +213,12 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
     for (int r = 0; r < 8; ++r) acc[i][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  load_stage(0);
+  load_stage(s_begin);
   store_stage(0);
   __syncthreads();
-  for (int s = 0; s < nstages; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nstages) load_stage(s + 1);
+  for (int s = s_begin; s < s_end; ++s) {
+    const int buf = (s - s_begin) & 1;
+    if (s + 1 < s_end) load_stage(s + 1);
     // All fragments of a 32-deep k step are read before its MFMAs, and the
     // next k step's fragments are read while they run, so the matrix core is
     // not left waiting on LDS between tiles.
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int r = 0; r < 8; ++r) acc[i][r] = mfma16x16x32<DT>(Af[ks & 1][i], Bf[ks & 1][r], acc[i][r]);
     }
-    if (s + 1 < nstages) store_stage(buf ^ 1);
+    if (s + 1 < s_end) store_stage(buf ^ 1);
     __syncthreads();
   }
 
@@ -253,14 +256,22 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + wm * WM + 16 * i + 4 * q + e;
-        if (m < p.M) p.y[(int64_t)m * p.N + n] = finish_output<DT>(acc[i][r][e], p.bias, (int)n);
+        if (m >= p.M) continue;
+        if (p.splits == 1)
+          p.y[(int64_t)m * p.N + n] = finish_output<DT>(acc[i][r][e], p.bias, (int)n);
+        else
+          p.partial[((int64_t)blockIdx.z * p.M + m) * p.N + n] = acc[i][r][e];
       }
     }
 }
 
 template <typename DT, int BM, int Z, int WAVES, int BK, int OCC>
-static void launch_prefill_t(const PrefillParams& p, bool dense, hipStream_t st) {
-  const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM);
+static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st) {
+  PrefillParams p = p0;  // K ranges of whole BK stages, none empty
+  const int nst = p.K / BK;
+  p.stages_per_split = (nst + p0.splits - 1) / p0.splits;
+  p.splits = (nst + p.stages_per_split - 1) / p.stages_per_split;
+  const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM, p.splits);
   if (dense)
     hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK, OCC>), grid, dim3(WAVES * 64), 0, st, p);
   else
@@ -285,6 +296,17 @@ int prefill_block_rows(int64_t M, int64_t N) {
   return col_blocks * ((M + 255) / 256) >= kTargetBlocks ? 256 : 128;
 }
 
+int prefill_splits(int64_t M, int64_t K, int64_t N) {
+  const int64_t BM = prefill_block_rows(M, N);
+  const int64_t blocks = ((N / 16 + 15) / 16) * ((M + BM - 1) / BM);
+  int64_t splits = (kTargetBlocks + blocks - 1) / blocks;
+  const int64_t by_k = K / 256;
+  if (splits > by_k) splits = by_k;
+  const int64_t by_bytes = (int64_t)kMaxPrefillPartialBytes / (M * N * 4);
+  if (splits > by_bytes) splits = by_bytes;
+  return splits > 1 ? (int)splits : 1;
+}
+
 // 64-row stages when K and the group size allow (more load latency hidden per
 // stage), else 32-row stages.
 template <typename DT>
@@ -299,8 +321,19 @@ static int launch_prefill_dt(const PrefillParams& p, int Z, bool dense, hipStrea
               : launch_prefill_bm<DT, 128, 8, 32>(p, Z, dense, st);
 }
 
-int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st) {
+// K ranges launch_prefill_t runs for an upper bound `splits` (whole stages).
+static int prefill_splits_run(const PrefillParams& p, int splits) {
+  const int BK = ((p.K % 64 == 0) && (p.gs % 64 == 0)) ? 64 : 32;
+  const int nst = p.K / BK;
+  const int sps = (nst + splits - 1) / splits;
+  return (nst + sps - 1) / sps;
+}
+
+int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, hipStream_t st,
+                   int* splits_run) {
   if (!dense && p.sigma == nullptr) return GRINQH_ERR_INVALID;
+  if (p.splits < 1 || (p.splits > 1 && p.partial == nullptr)) return GRINQH_ERR_INVALID;
+  *splits_run = prefill_splits_run(p, p.splits);
   const int Z = max_bits / 2;
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_prefill_dt<BF16>(p, Z, dense, st)
                                             : launch_prefill_dt<F16>(p, Z, dense, st);
