@@ -272,6 +272,24 @@ def test_prefill_split_k(graded, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0]],
+                         ids=["non_monotone", "skip_all", "all_planes", "tied"])
+def test_graded_prefill_grade_groups(t, dtype):
+    """The graded prefill consumes each scale group's rows ordered by zone set
+    (single-precision stages load and merge only their planes).  Zone sets
+    that are not prefixes, no active zone at all, every zone, and tied
+    thresholds must all give S10 within the weight-rounding bound."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    M, K, N, b = 100, 1024, 512, 8
+    rng = np.random.default_rng(321)
+    W, x, s = _setup(rng, K, N, b, dtype, M=M)
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), None, b, 128, N // 4, t)
+    pre = O.gemv_union_f64(x, W, s, t, b, 128)
+    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, b, 128, dtype), dtype, what=f"grade groups t={t}",
+                        extra_tol=graded_rounding_bound(x, W, s, t, b, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_256_row_tiles(dtype):
     """Enough blocks for the 256-row tile variant (64 column blocks x 4 row tiles)."""
     from grinqh.kernel import grinqh_prefill_dense

@@ -87,6 +87,11 @@ struct PrefillParams {
   int splits;            // grid.z: K ranges (1: y written directly)
   int stages_per_split;  // set by launch_prefill
   float* partial;        // [splits][M][N] fp32 when splits > 1 (the reduce kernel follows)
+  // graded, grade-grouped order (else nullptr): x holds the columns in this
+  // order, perm[k'] is the weight row of sorted position k' and
+  // stage_bits[k'/32] the zone-set union of each 32-row stage
+  const int* perm;
+  const uint32_t* stage_bits;
 };
 
 // Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.  p.splits
@@ -101,6 +106,12 @@ int prefill_block_rows(int64_t M, int64_t N);
 // only on (M, K, N), so the workspace size does too.
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
+
+// Grade-grouped order of the graded prefill (grade_order.hip).
+int launch_grade_order(const float* sigma, const GradeThresholds& thr, int K, int gs, int max_bits, int* perm,
+                       uint32_t* stage_bits, hipStream_t st);
+int launch_permute_cols(const uint16_t* x, int64_t ldx, const int* perm, int M, int K, uint16_t* xs,
+                        hipStream_t st);
 
 int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
 int launch_prepare_weight(const int8_t* W, uint32_t* out, int K, int N, int max_bits, hipStream_t st);

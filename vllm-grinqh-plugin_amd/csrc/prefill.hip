@@ -107,6 +107,22 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   float sig[RPT];
   uint16_t sraw[4 * JPT];  // scales of the stage's group when it starts a new group
   bool new_group = false;
+  // Grade-grouped order (graded batches, p.perm set): the weight rows of a
+  // stage come from perm, and planes outside the union of their zone sets are
+  // not fetched (past-the-end offsets read 0).  The order of stage s+1 is
+  // fetched while stage s is loaded, so the plane loads never wait on it.
+  int rows_nx[RPT];
+  uint32_t planes_nx = (1u << Z) - 1u;
+  auto fetch_order = [&](int s) {
+    if constexpr (!DENSE) {
+      if (p.perm == nullptr || s >= s_end) return;
+      const int k0 = s * BK;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) rows_nx[e] = p.perm[k0 + rg * RPT + e];
+      planes_nx = p.stage_bits[k0 >> 5];
+      if (BK == 64) planes_nx |= p.stage_bits[(k0 >> 5) + 1];
+    }
+  };
   auto load_stage = [&](int s) {
     const int k0 = s * BK;
     new_group = (s == s_begin) || (k0 / p.gs != (k0 - BK) / p.gs);
@@ -122,14 +138,30 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + k0 + 8 * piece) * 2) : 0x80000000u;
       xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
+    if constexpr (DENSE) {
 #pragma unroll
-    for (int e = 0; e < RPT; ++e) {
-      const int row = k0 + rg * RPT + e;
-      const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
+      for (int e = 0; e < RPT; ++e) {
+        const int row = k0 + rg * RPT + e;
+        const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
 #pragma unroll
-      for (int z = 0; z < Z; ++z)
-        D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
-      if (!DENSE) sig[e] = p.sigma[row];
+        for (int z = 0; z < Z; ++z)
+          D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
+      }
+    } else {
+      const bool grouped = p.perm != nullptr;
+      const uint32_t planes = planes_nx;
+#pragma unroll
+      for (int e = 0; e < RPT; ++e) {
+        const int row = grouped ? rows_nx[e] : k0 + rg * RPT + e;
+        const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
+#pragma unroll
+        for (int z = 0; z < Z; ++z) {
+          const uint32_t off = ((planes >> z) & 1u) ? rb + (uint32_t)z * p.NW * 4u : 0x80000000u;
+          D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)off, 0, 0);
+        }
+        sig[e] = p.sigma[row];
+      }
+      fetch_order(s + 1);
     }
   };
 
@@ -213,6 +245,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
     for (int r = 0; r < 8; ++r) acc[i][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  fetch_order(s_begin);
   load_stage(s_begin);
   store_stage(0);
   __syncthreads();
