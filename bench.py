@@ -115,6 +115,9 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=20, help="launches per case graph for kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-case", default=None, metavar="SHAPE:M:MODE",
+                    help="profiling run: one prefill product (e.g. gate_up:2048:union; MODE dense or union with "
+                         "t = [0, P70, P90, P98]) twice as warm-up and twice counted; prints no JSON line")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter-collection run: each decode case twice (eager) and a 256 MiB copy kernel "
                          "of known traffic for calibrating FETCH_SIZE / WRITE_SIZE; prints no JSON line")
@@ -133,6 +136,27 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"device {torch.cuda.get_device_name(dev)}")
+
+    if args.prefill_case:
+        name, m_str, mode = args.prefill_case.split(":")
+        K, N = {n: (k, nn) for n, k, nn in SHAPES}[name]
+        M = int(m_str)
+        w, s = synth_weight(torch, K, N, 1000, dev)
+        P = prepare_weight(w, BITS)
+        x = synth_x(torch, M, K, 5, dev)
+        t = thresholds_for(x, (0.7, 0.9, 0.98)) if mode == "union" else [0.0] * 4
+        for _ in range(2):
+            run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(2):
+            run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 2
+        log(f"prefill case {name} M={M} {mode}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s")
+        return 0
 
     # ---------------- weights (rotated copies to defeat the MALL)
     base = {}

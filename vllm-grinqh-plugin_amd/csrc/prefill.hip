@@ -347,9 +347,13 @@ static int launch_prefill_dt(const PrefillParams& p, int Z, bool dense, hipStrea
   // 256-row tiles: one wave per SIMD (128 x 128 per wave); 128-row tiles: two
   // waves per SIMD (32 x 128 per wave), whose dequantization and MFMAs overlap.
   const bool bk64 = (p.K % 64 == 0) && (p.gs % 64 == 0);
-  if (prefill_block_rows(p.M, p.N) == 256)
-    return bk64 ? launch_prefill_bm<DT, 256, 4, 64>(p, Z, dense, st)
-                : launch_prefill_bm<DT, 256, 4, 32>(p, Z, dense, st);
+  // (bf16's fp32 dequantization does not fit the 256-row tile's registers:
+  // it always takes 128-row tiles)
+  if constexpr (DT::id == F16::id) {
+    if (prefill_block_rows(p.M, p.N) == 256)
+      return bk64 ? launch_prefill_bm<DT, 256, 4, 64>(p, Z, dense, st)
+                  : launch_prefill_bm<DT, 256, 4, 32>(p, Z, dense, st);
+  }
   return bk64 ? launch_prefill_bm<DT, 128, 8, 64>(p, Z, dense, st)
               : launch_prefill_bm<DT, 128, 8, 32>(p, Z, dense, st);
 }
