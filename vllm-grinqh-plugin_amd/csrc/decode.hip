@@ -250,10 +250,13 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   };
 
   // one tile: optional prefetch of tile t+2, unpack, MFMA, group epilogue
+  // position of the current tile in its scale group and the group's index in
+  // the staged scales, advanced per tile (no divisions in the loop)
+  int gpos = (tile0 + t_begin) % tiles_per_group;
+  int gloc = (tile0 + t_begin) / tiles_per_group - g_first;
   auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn) {
-    const int gt = tile0 + t;  // absolute tile
-    const bool first_of_group = (t == t_begin) || (gt % tiles_per_group == 0);
-    const bool last_of_group = (t + 1 == t_end) || ((gt + 1) % tiles_per_group == 0);
+    const bool first_of_group = (t == t_begin) || (gpos == 0);
+    const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
     if (prefetch) issue(t + 2, Tn);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -307,7 +310,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       Cv[mt] = mfma16x16x32<DT>(A[mt], bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv[mt]);
 
     if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv), scales from LDS
-      const uint16_t* srow = &s_scale[(gt / tiles_per_group - g_first) * 256 + 64 * jg * NJ + c];
+      const uint16_t* srow = &s_scale[gloc * 256 + 64 * jg * NJ + c];
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
@@ -318,6 +321,12 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) Y[mt][jj][b][e] = fmaf(sc, C[mt][jj][b][e] + Cv[mt][e], Y[mt][jj][b][e]);
         }
+    }
+    if (gpos + 1 == tiles_per_group) {
+      gpos = 0;
+      ++gloc;
+    } else {
+      ++gpos;
     }
   };
 

@@ -221,10 +221,14 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     }
   };
 
+  // position of the current tile in its scale group and the group's index in
+  // the staged scales, advanced per tile (no divisions in the loop)
+  const int tiles_per_group = p.gs / TR;
+  int gpos = (row0 / TR + t_begin) % tiles_per_group;
+  int gloc = (row0 + TR * t_begin) / p.gs - g_first;
   auto step = [&](int t, uint32_t (&Dc)[TR][Z], bool prefetch, uint32_t (&Dn)[TR][Z]) {
-    const int rowa = row0 + TR * t;
-    const bool first_of_group = (t == t_begin) || (rowa % p.gs == 0);
-    const bool last_of_group = (t + 1 == t_end) || ((rowa + TR) % p.gs == 0);
+    const bool first_of_group = (t == t_begin) || (gpos == 0);
+    const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
     if (prefetch) issue(t + 2, Dn);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     Cv = tile_mfma<DT, TR>(A, bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv);
 
     if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv)
-      const uint16_t* srow = &s_scale[(rowa / p.gs - g_first) * 1024 + lane];
+      const uint16_t* srow = &s_scale[gloc * 1024 + lane];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -267,6 +271,12 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
 #pragma unroll
           for (int i = 0; i < MR; ++i) Y[j][b][i] = fmaf(sc, C[j][b][i] + Cv[i], Y[j][b][i]);
         }
+    }
+    if (gpos + 1 == tiles_per_group) {
+      gpos = 0;
+      ++gloc;
+    } else {
+      ++gpos;
     }
   };
 

@@ -50,16 +50,17 @@ __device__ __forceinline__ void splitk_complete(const DecodeParams& p, int cb, i
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       p.partial, (short)0, (int)(slab * (uint32_t)p.splits), 0x00020000);
 
-  uint32_t off[NCK];
-  int64_t out[NCK];
+  uint32_t off[NCK];  // byte offset of the chunk in a K range's slab; bit 31: none (reads 0)
+  int col[NCK];       // first output column of the chunk
 #pragma unroll
   for (int k = 0; k < NCK; ++k) {
     const int i = threadIdx.x + 256 * k;
-    const int m = i / per_m, rem = i % per_m;
-    const int wcol = w0 + 4 * (rem % cpr);
+    const int m = i / per_m, rem = i - m * per_m;
+    const int r = rem / cpr;
+    const int wcol = w0 + 4 * (rem - r * cpr);
     const bool ok = i < total && wcol < p.NW;
-    out[k] = ok ? (int64_t)m * p.N + (int64_t)(rem / cpr) * p.NW + wcol : -1;
-    off[k] = ok ? (uint32_t)out[k] * 4u : 0x80000000u;  // bit 31: past the end, reads 0
+    col[k] = r * p.NW + wcol;
+    off[k] = ok ? ((uint32_t)m * (uint32_t)p.N + (uint32_t)col[k]) * 4u : 0x80000000u;
   }
   f32x4_t acc[NCK];
 #pragma unroll
@@ -81,12 +82,12 @@ __device__ __forceinline__ void splitk_complete(const DecodeParams& p, int cb, i
   }
 #pragma unroll
   for (int k = 0; k < NCK; ++k) {
-    if (out[k] < 0) continue;
-    const int n = (int)(out[k] % p.N);
+    if (off[k] == 0x80000000u) continue;
+    const int n = col[k];
     u32x2_t h;
     h[0] = (uint32_t)finish_output<DT>(acc[k][0], p.bias, n) | ((uint32_t)finish_output<DT>(acc[k][1], p.bias, n + 1) << 16);
     h[1] = (uint32_t)finish_output<DT>(acc[k][2], p.bias, n + 2) | ((uint32_t)finish_output<DT>(acc[k][3], p.bias, n + 3) << 16);
-    *reinterpret_cast<u32x2_t*>(p.y + out[k]) = h;
+    *reinterpret_cast<u32x2_t*>(p.y + (off[k] >> 2)) = h;
   }
   if (threadIdx.x == 0) atomicExch(&p.counters[cb], 0u);
 }
