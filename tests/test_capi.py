@@ -40,6 +40,14 @@ def test_version_and_status_strings(lib):
     assert lib.grinqh_status_string(99) == b"unknown status"
 
 
+def test_library_path_honours_environment(monkeypatch):
+    from grinqh import _lib
+    monkeypatch.setenv("GRINQH_LIB", "/opt/elsewhere/libgrinqh_hip.so")
+    assert _lib.library_path() == "/opt/elsewhere/libgrinqh_hip.so"
+    monkeypatch.delenv("GRINQH_LIB")
+    assert _lib.library_path().endswith("libgrinqh_hip.so")
+
+
 def test_workspace_query(lib):
     # M=1 o_proj shape: split-K needs one fp32 [M][N] slab per K range.
     ws = lib.grinqh_workspace_bytes(1, 4096, 4096, 8, 0)

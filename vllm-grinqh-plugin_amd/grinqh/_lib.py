@@ -55,7 +55,8 @@ _lib = None
 
 
 def library_path() -> str:
-    return _LIB_PATH
+    """The in-tree build, or the library named by the GRINQH_LIB environment variable."""
+    return os.environ.get("GRINQH_LIB") or _LIB_PATH
 
 
 def load_library(path: str | None = None) -> ctypes.CDLL:
@@ -64,7 +65,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None and path is None:
             return _lib
-        p = path or _LIB_PATH
+        p = path or library_path()
         if not os.path.exists(p):
             raise RuntimeError(
                 f"GRINQH HIP library not found at {p}; build it with "
