@@ -14,8 +14,9 @@ by the grading + scales + x + y) per second.  The JSON line also carries the
 per-case kernel times, the roofline of the dominant kernel, the prefill
 TFLOP/s at M=2048 (dense, the reference's dispatch for M > 1), the graded
 prefill sweep of BASELINE configs[2] (M = 512, 2048, 8192, 70/20/8/2 % grade
-mix) and the CPU baseline (the reference's pure-PyTorch math on the host
-cores).
+mix), the Llama-3-70B shapes of BASELINE configs[4] with every zone active
+(M = 1, 64, 4096) and the CPU baseline (the reference's pure-PyTorch math on
+the host cores).
 """
 from __future__ import annotations
 
@@ -40,6 +41,9 @@ SHAPES = [("qkv", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up", 4096, 28672),
 DECODE_M = [1, 4, 16, 64]
 PREFILL_M = 2048
 PREFILL_GRADED_M = (512, 2048, 8192)
+# Llama-3-70B linear shapes, M in {1, 64, 4096}, every zone active
+SHAPES_70B = [("qkv", 8192, 10240), ("gate_up", 8192, 57344), ("down", 28672, 8192)]
+M_70B = (1, 64, 4096)
 GS = 128
 BITS = 8
 MALL_BYTES = 256 << 20
@@ -115,6 +119,7 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=20, help="launches per case graph for kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B shape sweep (BASELINE configs[4])")
     ap.add_argument("--prefill-case", default=None, metavar="SHAPE:M:MODE",
                     help="profiling run: one prefill product (e.g. gate_up:2048:union; MODE dense or union with "
                          "t = [0, P70, P90, P98]) twice as warm-up and twice counted; prints no JSON line")
@@ -348,6 +353,50 @@ def main() -> int:
                 log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
                 del x
 
+    # ---------------- Llama-3-70B shapes, adversarial grading (thresholds -1:
+    # every token exceeds every threshold, so every plane is read); M <= 64 as GB/s, M = 4096 as TFLOP/s
+    big = None
+    if not args.no_70b:
+        big = []
+        for i, (name, K, N) in enumerate(SHAPES_70B):
+            w, s = synth_weight(torch, K, N, 2000 + i, dev)
+            p0 = prepare_weight(w, BITS)
+            del w
+            cps = [(p0, s), (p0.clone(), s.clone())]  # two copies of >= 168 MB rotate past the MALL
+            for M in M_70B:
+                x = synth_x(torch, M, K, 299 + i, dev)
+                t = [-1.0] * 4
+                n_it = 4
+                with torch.cuda.stream(stream):
+                    for j in range(2):
+                        run_product(x, cps[j][0], cps[j][1], None, BITS, GS, N // 4, t, "union")
+                    torch.cuda.synchronize()
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=stream):
+                        for j in range(n_it):
+                            run_product(x, cps[j % 2][0], cps[j % 2][1], None, BITS, GS, N // 4, t, "union")
+                    g.replay()
+                    torch.cuda.synchronize()
+                    e0.record(stream)
+                    for _ in range(3):
+                        g.replay()
+                    e1.record(stream)
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (3 * n_it)
+                rec = {"shape": name, "K": K, "N": N, "M": M, "us": round(us, 2)}
+                if M <= 64:
+                    b = decode_bytes(np.full(K, BITS // 2), K, N, M)
+                    rec.update(bytes=b, gbs=round(b / (us * 1e-6) / 1e9, 1), frac=round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+                    log(f"70B {name:8s} M={M:5d} {us:9.1f} us {rec['gbs']:8.1f} GB/s ({100 * rec['frac']:.1f}% HBM)")
+                else:
+                    tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
+                    rec.update(tflops=round(tf, 1), frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
+                    log(f"70B {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
+                big.append(rec)
+                del g, x
+            del cps, p0, s
+            torch.cuda.empty_cache()
+
     # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores
     cpu = None
     if not args.no_cpu_baseline:
@@ -387,6 +436,7 @@ def main() -> int:
                   for c in cases],
         "prefill": prefill,
         "prefill_graded": prefill_graded,
+        "llama70b_adversarial": big,
     }
     print(json.dumps(out), flush=True)
     return 0
