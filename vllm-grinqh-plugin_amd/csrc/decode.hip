@@ -45,11 +45,27 @@ namespace grinqh {
 
 constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged in LDS)
 
+// 33-64 rows in fp16 ("scaled" path) multiply the scaled weight RNE(w * s),
+// built in registers as the prefill builds it in LDS, and accumulate the
+// output directly: no per-group partial sums, no correction column, no group
+// epilogue.  The registers this frees let a wave cover two output dwords of all
+// 64 rows (128 sums per lane), so the four waves are two output-dword pairs x
+// two K sub-ranges: each plane word and x element is loaded and unpacked by two
+// waves instead of four.  The weight is rounded once to fp16, as in the
+// reference's dense path (grinqh/kernel.py:586).
+template <typename DT, int MT>
+constexpr bool decode_scaled() { return MT == 4 && DT::id == F16::id; }
+
 template <typename DT, int MT, int Z, bool DENSE>
 __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
+  constexpr bool SC = decode_scaled<DT, MT>();
+  constexpr int NT = 256;      // threads per block
   constexpr int MP = 16 * MT;  // padded rows of x
-  constexpr int NJ = 4 / MT;   // output dwords j per wave
-  constexpr int KW = 4 / MT;   // K sub-ranges per block
+  constexpr int NJ = SC ? 2 : 4 / MT;  // output dwords j per wave
+  constexpr int KW = SC ? 2 : 4 / MT;  // K sub-ranges per block
+  constexpr int JG = 4 / KW;           // groups of output dwords (waves per K sub-range)
+  constexpr int SLOTS = MT * NJ * 4;   // f32x4 output sums per lane
+  constexpr int PF = 2;                // tiles of loads in flight ahead of the one unpacked
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
   // A operand is read from global memory (L2-resident) with the plane words,
@@ -60,12 +76,12 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   constexpr int XS = RMAX + 8;  // halves per staged x row (16-byte rows, banks staggered)
   constexpr int X_BYTES = AG ? 0 : MP * XS * 2;
   constexpr int OFF_BYTES = RMAX * Z * 4;
-  constexpr int RED_VECS = (KW - 1) * MT * 16 * 64;  // f32x4 slots for the in-block reduction
+  constexpr int RED_VECS = (KW - 1) * JG * SLOTS * 64;  // f32x4 slots for the in-block reduction
   constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_VECS * 16 ? (X_BYTES + OFF_BYTES) : RED_VECS * 16;
   constexpr int SC_GROUPS = RMAX / 32 + 1;  // scale groups a K range can touch (group size >= 32)
   constexpr int CPR = RMAX / 8;             // 16-byte x chunks per staged row
-  constexpr int XPT = AG ? 1 : MP * CPR / 256;  // x chunks per thread
-  constexpr int SPT = (SC_GROUPS * 32 + 255) / 256;  // 16-byte scale chunks per thread
+  constexpr int XPT = AG ? 1 : MP * CPR / NT;  // x chunks per thread
+  constexpr int SPT = (SC_GROUPS * 32 + NT - 1) / NT;  // 16-byte scale chunks per thread
 
   // staging area: x rows and (row, plane) offsets; reused for the in-block reduction
   __shared__ __align__(16) unsigned char s_pool[POOL_BYTES];
@@ -78,7 +94,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int jg = wave % MT, kw = wave / MT;
+  const int jg = wave % JG, kw = wave / JG;
   const int c = lane & 15, q = lane >> 4;
   // logical block = (column block, K range), column blocks fastest, ranges of
   // consecutive logical blocks per XCD (adjacent column blocks share lines)
@@ -118,7 +134,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     u32x4_t sv[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
-      const int h = tid + 256 * k;  // (group, tile, half) chunk
+      const int h = tid + NT * k;  // (group, tile, half) chunk
       const int gl = h >> 5, r = (h >> 1) & 15, hf = h & 1;
       const uint32_t off =
           (gl < n_groups && vec_scales)
@@ -135,11 +151,11 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     }
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
-      const int h = tid + 256 * k;
+      const int h = tid + NT * k;
       if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
     }
     if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
-      for (int idx = tid; idx < n_groups * 256; idx += 256) {
+      for (int idx = tid; idx < n_groups * 256; idx += NT) {
         const int gl = idx >> 8, col = idx & 255;
         const int wcol = min(w0 + (col & 15), p.NW - 1);
         s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)(col >> 4) * p.NW + wcol];
@@ -154,7 +170,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   // the 128); other rows have bit 7 clear and need no flip:
   //   w_eff * 2^sh = u + beta * 2^sh - (zone 0 active ? 128 : 0).
   // A row with no active zone therefore contributes exact zeros.
-  for (int rr = tid; rr < R; rr += 256) {
+  for (int rr = tid; rr < R; rr += NT) {
     uint32_t bits;
     if (DENSE) {
       bits = (1u << Z) - 1u;
@@ -169,7 +185,10 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       bits = zone_bits<Z>(s, p.thr.t);
     }
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
-    s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - ((bits & 1u) ? 128 : 0));
+    if constexpr (SC)  // -c_row of the scaled weight (u >> sh) - c_row, an exact fp16 integer
+      s_bv[rr] = f32_to_f16_bits(-(float)(1024 + ((bits & 1u) ? (128 >> SH) : 0) - beta));
+    else
+      s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - ((bits & 1u) ? 128 : 0));
     s_xm[rr] = zone0_flip(bits);
     const uint32_t row_bytes = (uint32_t)(row0 + rr) * (uint32_t)(Z * p.NW) * 4u;
 #pragma unroll
@@ -254,10 +273,11 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   // the staged scales, advanced per tile (no divisions in the loop)
   int gpos = (tile0 + t_begin) % tiles_per_group;
   int gloc = (tile0 + t_begin) / tiles_per_group - g_first;
+  uint32_t s2[NJ][4];  // scaled path: (s, s) of the current group's columns
   auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn) {
     const bool first_of_group = (t == t_begin) || (gpos == 0);
     const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
-    if (prefetch) issue(t + 2, Tn);
+    if (prefetch) issue(t + PF, Tn);
     __builtin_amdgcn_sched_barrier(0);
 
     const int sb = t * 32 + 8 * q;
@@ -285,8 +305,32 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       }
     }
     prepare_planes<Z>(Tc.D, xm);
+    if constexpr (SC) {
+      // B = RNE(w * s) with s2 = (s, s) of this lane's columns for the group
+      // and bv = (-c_row, -c_row') per row pair; the output accumulates directly.
+      if (first_of_group) {
+        const uint16_t* srow = &s_scale[gloc * 256 + 64 * jg * NJ + c];
 #pragma unroll
-    for (int jj = 0; jj < NJ; ++jj) {
+        for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) s2[jj][b] = (uint32_t)srow[(4 * jj + b) * 16] * 0x00010001u;
+      }
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) {
+        uint32_t V[8];
+        code_dwords<Z>(Tc.D, jg * NJ + jj, V);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          u32x4_t B;
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) B[pp] = Dequant<F16, SH>::pair(V[2 * pp], V[2 * pp + 1], b, bv[pp], s2[jj][b]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) Y[mt][jj][b] = mfma16x16x32<DT>(A[mt], B, Y[mt][jj][b]);
+        }
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < (SC ? 0 : NJ); ++jj) {
       const int j = jg * NJ + jj;
       uint32_t V[8];
       code_dwords<Z>(Tc.D, j, V);
@@ -306,10 +350,10 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < (SC ? 0 : MT); ++mt)
       Cv[mt] = mfma16x16x32<DT>(A[mt], bv, first_of_group ? f32x4_t{0.f, 0.f, 0.f, 0.f} : Cv[mt]);
 
-    if (last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv), scales from LDS
+    if (!SC && last_of_group) {  // y += s[g][n] * 2^-sh * (C + Cv), scales from LDS
       const uint16_t* srow = &s_scale[gloc * 256 + 64 * jg * NJ + c];
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
@@ -331,19 +375,29 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   };
 
   {
-    // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
     Tile TA, TB, TC;
-    issue(t_begin, TA);
-    issue(t_begin + 1, TB);
     int t = t_begin;
-    for (; t + 3 <= t_end; t += 3) {
-      step(t, TA, true, TC);
-      step(t + 1, TB, true, TA);
-      step(t + 2, TC, true, TB);
+    if constexpr (PF == 2) {
+      // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
+      issue(t_begin, TA);
+      issue(t_begin + 1, TB);
+      for (; t + 3 <= t_end; t += 3) {
+        step(t, TA, true, TC);
+        step(t + 1, TB, true, TA);
+        step(t + 2, TC, true, TB);
+      }
+      // at most two tiles left, already loaded into TA and TB
+      if (t < t_end) step(t, TA, false, TC);
+      if (t + 1 < t_end) step(t + 1, TB, false, TC);
+    } else {
+      // two tile buffers: tile t+1 is in flight while tile t is unpacked
+      issue(t_begin, TA);
+      for (; t + 2 <= t_end; t += 2) {
+        step(t, TA, true, TB);
+        step(t + 1, TB, true, TA);
+      }
+      if (t < t_end) step(t, TA, false, TB);
     }
-    // at most two tiles left, already loaded into TA and TB
-    if (t < t_end) step(t, TA, false, TC);
-    if (t + 1 < t_end) step(t + 1, TB, false, TC);
   }
 
   // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...
@@ -351,7 +405,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   if (KW > 1) {
     __syncthreads();
     if (kw > 0) {
-      f32x4_t* slot = s_red + ((kw - 1) * MT + jg) * 16 * 64;
+      f32x4_t* slot = s_red + ((kw - 1) * JG + jg) * SLOTS * 64;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -363,7 +417,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     if (kw == 0) {
 #pragma unroll
       for (int k2 = 1; k2 < KW; ++k2) {
-        const f32x4_t* slot = s_red + ((k2 - 1) * MT + jg) * 16 * 64;
+        const f32x4_t* slot = s_red + ((k2 - 1) * JG + jg) * SLOTS * 64;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -493,7 +547,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   const int64_t NW = N / 16;
   pl.col_blocks = (int)((NW + 15) / 16);
   const int64_t T = K / 32;
-  const int kw = 4 / pl.mt;
+  const int kw = pl.mt == 4 ? 2 : 4 / pl.mt;  // K sub-ranges per block (two on the scaled path)
   const int64_t tiles_max = (pl.mt >= 2 ? kDecodeRowsPerBlock : kDecodeRowsPerBlock / pl.mt) / 32;
   const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
   // one block per CU, all blocks resident at once: the per-block set-up

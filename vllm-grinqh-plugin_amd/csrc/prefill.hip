@@ -26,40 +26,6 @@
 
 namespace grinqh {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-
-// Two rows (low half = row 0, high half = row 1) of column tile beta from the
-// code dwords V0, V1 (offset-binary bytes u): RNE(w * s) with
-// w = (u >> sh) - c_row, c_row = 1024 + (128 >> sh) - beta_row.
-template <typename DT, int SH>
-struct Dequant;
-
-template <int SH>
-struct Dequant<F16, SH> {
-  // negc: (-c_row0, -c_row1) as fp16; s2: (s, s) as fp16
-  __device__ __forceinline__ static uint32_t pair(uint32_t V0, uint32_t V1, int beta, uint32_t negc, uint32_t s2) {
-    uint32_t h = perm(V1, V0, 0x0C040C00u + (uint32_t)beta * 0x00010001u);  // (u0, 0, u1, 0)
-    if (SH > 0) h >>= SH;  // the low sh bits of each code byte are zero, so halves do not mix
-    h |= 0x64006400u;      // 1024 + (u >> sh), exact
-    const half2_t w = __builtin_bit_cast(half2_t, h) + __builtin_bit_cast(half2_t, negc);  // exact integers
-    return __builtin_bit_cast(uint32_t, w * __builtin_bit_cast(half2_t, s2));                // RNE(w * s)
-  }
-};
-
-template <int SH>
-struct Dequant<BF16, SH> {
-  // negc: per row -c_row * 2^sh... carried as two floats in the caller; here
-  // w * s = (u - C_row) * (s * 2^-sh) with C_row = 128 - beta_row * 2^sh: exact
-  // in fp32, then one rounding to bf16.
-  __device__ __forceinline__ static uint32_t pair_bf16(uint32_t V0, uint32_t V1, int beta, float c0, float c1,
-                                                       float s_sh) {
-    const float a = (float)((V0 >> (8 * beta)) & 0xFFu) - c0;
-    const float b = (float)((V1 >> (8 * beta)) & 0xFFu) - c1;
-    return (uint32_t)f32_to_bf16_bits(a * s_sh) | ((uint32_t)f32_to_bf16_bits(b * s_sh) << 16);
-  }
-};
-
 // One block: BM rows x 256 logical columns; WAVES waves as (WAVES/2) x 2, each
 // BM/(WAVES/2) rows x 8 column tiles.  A stage is BK rows of K: its global
 // loads are issued before the previous stage's MFMAs and consumed after them,
