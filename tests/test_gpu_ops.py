@@ -392,6 +392,38 @@ def test_split_k_counters_return_to_zero():
                             what=f"M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("mode", ["union", "dense"])
+@pytest.mark.parametrize("M", [40, 64, 130])
+def test_large_scales_round_once(M, mode):
+    """Scales of +-200 in one group next to ordinary ones (|w*s| up to ~2.6e4,
+    near the fp16 range of the rounded weight) still give the oracle's product
+    within the weight-rounding bound, on the fp16 kernels that round w*s to
+    fp16 (33-64-row decode, prefill) in both grading modes."""
+    from grinqh.kernel import grinqh_gemv_batch_union, grinqh_prefill_dense
+    rng = np.random.default_rng(500 + M)
+    K, N, b, dtype = 512, 768, 8, "float16"
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)) * 1e-3, dtype)
+    s = rng.standard_normal((K // 128, N)) * 0.05
+    s[1, :200] = np.where(rng.random(200) < 0.5, -200.0, 200.0)
+    s = to_dtype_np(s, dtype)
+    P, xt, st = _prepare(W, b), _tdt(x, dtype), _tdt(s, dtype)
+    if mode == "union":
+        sigma = np.abs(x).max(0).astype(np.float32)
+        t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+        y = grinqh_gemv_batch_union(xt, P, st, None, b, 128, N // 4, t)
+        pre = O.gemv_union_f64(x, W, s, t, b, 128)
+        fin = O.gemv_union(x, W, s, None, t, b, 128, dtype)
+        extra = graded_rounding_bound(x, W, s, t, b, dtype)
+    else:
+        y = grinqh_prefill_dense(xt, P, st, 128, N // 4, b)
+        pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+        fin = O.dense_prefill(x, W, s, None, 128, dtype)
+        extra = dense_rounding_bound(x, W, s, dtype)
+    assert np.isfinite(fin).all()
+    assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}", extra_tol=extra)
+
+
 @pytest.mark.parametrize("M", [1, 3, 20])
 def test_nonfinite_rows_poison_their_output_row(M):
     """A NaN or inf activation makes its whole output row NaN, as the
