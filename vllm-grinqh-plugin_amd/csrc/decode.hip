@@ -55,17 +55,23 @@ constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged
 // reference's dense path (grinqh/kernel.py:586).
 template <typename DT, int MT>
 constexpr bool decode_scaled() { return MT == 4 && DT::id == F16::id; }
+template <typename DT, int MT>
+constexpr int decode_waves() { return decode_scaled<DT, MT>() ? 8 : 4; }
 
 template <typename DT, int MT, int Z, bool DENSE>
-__global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kernel(DecodeParams p) {
   constexpr bool SC = decode_scaled<DT, MT>();
-  constexpr int NT = 256;      // threads per block
-  constexpr int MP = 16 * MT;  // padded rows of x
+  constexpr int NWV = decode_waves<DT, MT>();
+  constexpr int NT = 64 * NWV;         // threads per block
+  constexpr int MP = 16 * MT;          // padded rows of x
   constexpr int NJ = SC ? 2 : 4 / MT;  // output dwords j per wave
-  constexpr int KW = SC ? 2 : 4 / MT;  // K sub-ranges per block
-  constexpr int JG = 4 / KW;           // groups of output dwords (waves per K sub-range)
-  constexpr int SLOTS = MT * NJ * 4;   // f32x4 output sums per lane
-  constexpr int PF = 2;                // tiles of loads in flight ahead of the one unpacked
+  constexpr int KW = SC ? 4 : 4 / MT;  // K sub-ranges per block
+  constexpr int JG = NWV / KW;         // groups of output dwords (waves per K sub-range)
+  // tiles of loads in flight ahead of the one unpacked; the scaled path runs
+  // two waves per SIMD on 256 registers, with one tile ahead and its A operand
+  // loaded when the tile starts
+  constexpr int PF = SC ? 1 : 2;
+  constexpr bool A_LATE = SC;
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
   // A operand is read from global memory (L2-resident) with the plane words,
@@ -76,7 +82,8 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   constexpr int XS = RMAX + 8;  // halves per staged x row (16-byte rows, banks staggered)
   constexpr int X_BYTES = AG ? 0 : MP * XS * 2;
   constexpr int OFF_BYTES = RMAX * Z * 4;
-  constexpr int RED_VECS = (KW - 1) * JG * SLOTS * 64;  // f32x4 slots for the in-block reduction
+  // f32x4 slots for the in-block reduction, done one m-tile at a time
+  constexpr int RED_VECS = (KW - 1) * JG * NJ * 4 * 64;
   constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_VECS * 16 ? (X_BYTES + OFF_BYTES) : RED_VECS * 16;
   constexpr int SC_GROUPS = RMAX / 32 + 1;  // scale groups a K range can touch (group size >= 32)
   constexpr int CPR = RMAX / 8;             // 16-byte x chunks per staged row
@@ -233,7 +240,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
   // plane words of one tile (and, above 16 rows, its A operand)
   struct Tile {
     uint32_t D[8][Z];
-    u32x4_t A[AG ? MT : 1];
+    u32x4_t A[AG && !A_LATE ? MT : 1];
   };
   const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
         T.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
       }
     }
-    if constexpr (AG) {  // x[16*mt + c][rows 8q .. 8q+7 of the tile]; rows m >= M read 0
+    if constexpr (AG && !A_LATE) {  // x[16*mt + c][rows 8q .. 8q+7 of the tile]; rows m >= M read 0
       const __amdgpu_buffer_rsrc_t xs = live ? xsrc : xsrc_none;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -287,10 +294,15 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     u32x4_t A[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if constexpr (AG)
+      if constexpr (A_LATE) {  // rows m >= M read 0
+        const int m = 16 * mt + c;
+        const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + sb) * 2) : 0x80000000u;
+        A[mt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
+      } else if constexpr (AG) {
         A[mt] = Tc.A[mt];
-      else
+      } else {
         A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
+      }
     }
 
     // Rebuild the code bytes (offset binary) and turn them into B operands.
@@ -400,30 +412,30 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
     }
   }
 
-  // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...
-  // (the staging area is free now and holds one slot per contributing wave)
+  // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...,
+  // one m-tile per round (the staging area is free now and holds one slot per
+  // contributing wave)
   if (KW > 1) {
-    __syncthreads();
-    if (kw > 0) {
-      f32x4_t* slot = s_red + ((kw - 1) * JG + jg) * SLOTS * 64;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      __syncthreads();
+      if (kw > 0) {
+        f32x4_t* slot = s_red + ((kw - 1) * JG + jg) * NJ * 4 * 64;
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) slot[((mt * NJ + jj) * 4 + b) * 64 + lane] = Y[mt][jj][b];
-    }
-    __syncthreads();
-    if (kw == 0) {
+          for (int b = 0; b < 4; ++b) slot[(jj * 4 + b) * 64 + lane] = Y[mt][jj][b];
+      }
+      __syncthreads();
+      if (kw == 0) {
 #pragma unroll
-      for (int k2 = 1; k2 < KW; ++k2) {
-        const f32x4_t* slot = s_red + ((k2 - 1) * JG + jg) * SLOTS * 64;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int k2 = 1; k2 < KW; ++k2) {
+          const f32x4_t* slot = s_red + ((k2 - 1) * JG + jg) * NJ * 4 * 64;
 #pragma unroll
           for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) Y[mt][jj][b] += slot[((mt * NJ + jj) * 4 + b) * 64 + lane];
+            for (int b = 0; b < 4; ++b) Y[mt][jj][b] += slot[(jj * 4 + b) * 64 + lane];
+        }
       }
     }
   }
@@ -466,7 +478,7 @@ __global__ __launch_bounds__(256, 1) void decode_kernel(DecodeParams p) {
             if (m < p.M) store_partial(&part[(int64_t)m * p.N + col_of(jj, b)], Y[mt][jj][b][e]);
           }
   }
-  if (p.counters != nullptr) splitk_complete<DT, 4 * MT>(p, lb % col_blocks, w0, 16);
+  if (p.counters != nullptr) splitk_complete<DT, 4 * MT * 256 / NT, NT>(p, lb % col_blocks, w0, 16);
 }
 
 // y[m][n] = cast(sum_{s=0..splits-1} partial[s][m][n]) (+ bias), four
@@ -547,7 +559,7 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
   const int64_t NW = N / 16;
   pl.col_blocks = (int)((NW + 15) / 16);
   const int64_t T = K / 32;
-  const int kw = pl.mt == 4 ? 2 : 4 / pl.mt;  // K sub-ranges per block (two on the scaled path)
+  const int kw = pl.mt == 4 ? 4 : 4 / pl.mt;  // K sub-ranges per block (four on the scaled path)
   const int64_t tiles_max = (pl.mt >= 2 ? kDecodeRowsPerBlock : kDecodeRowsPerBlock / pl.mt) / 32;
   const int64_t min_splits = (T + tiles_max - 1) / tiles_max;
   // one block per CU, all blocks resident at once: the per-block set-up
@@ -577,10 +589,11 @@ DecodePlan plan_decode(int64_t M, int64_t K, int64_t N) {
 template <typename DT, int MT, int Z>
 static void launch_decode_t(const DecodeParams& p, const DecodePlan& pl, bool dense, hipStream_t st) {
   const dim3 grid(pl.col_blocks * pl.splits);
+  const dim3 block(64 * decode_waves<DT, MT>());
   if (dense)
-    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, true>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, true>), grid, block, 0, st, p);
   else
-    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, false>), grid, block, 0, st, p);
 }
 
 template <typename DT, int MT>

@@ -32,8 +32,8 @@ __device__ __forceinline__ void store_partial(float* dst, float v) {
 // Columns of one column block: r * NW + w0 + [0, width) for column tiles
 // r = 0..15, clipped at NW (NW % 4 == 0, so a 4-column chunk is either wholly
 // inside or wholly outside).  NCK = 4-column chunks per thread (the block's
-// M * 16 * width / 4 chunks over 256 threads, rounded up).
-template <typename DT, int NCK>
+// M * 16 * width / 4 chunks over the block's NT threads, rounded up).
+template <typename DT, int NCK, int NT = 256>
 __device__ __forceinline__ void splitk_complete(const DecodeParams& p, int cb, int w0, int width) {
   constexpr int SB = 16 / NCK;  // K ranges per round: 16 loads in flight per thread
   __shared__ int s_last;
@@ -54,7 +54,7 @@ __device__ __forceinline__ void splitk_complete(const DecodeParams& p, int cb, i
   int col[NCK];       // first output column of the chunk
 #pragma unroll
   for (int k = 0; k < NCK; ++k) {
-    const int i = threadIdx.x + 256 * k;
+    const int i = threadIdx.x + NT * k;
     const int m = i / per_m, rem = i - m * per_m;
     const int r = rem / cpr;
     const int wcol = w0 + 4 * (rem - r * cpr);
