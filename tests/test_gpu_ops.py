@@ -50,8 +50,8 @@ def rounds_weight(M, dtype):
     """Whether the kernel serving an M-row graded batch rounds w_eff*s to the
     activation dtype (as the reference's dense path does) instead of applying
     the scale in fp32: the prefill kernel above 64 rows, and the fp16 decode
-    kernel for 33-64 rows."""
-    return M > 64 or (M > 32 and dtype == "float16")
+    kernel for 17-64 rows."""
+    return M > 64 or (M > 16 and dtype == "float16")
 
 
 def _tdt(x, dtype):
@@ -228,7 +228,7 @@ def test_union_graded_batches(M, max_bits, dtype):
     t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128, 192, t)
     pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
-    # the prefill kernel (above 64 rows) and the fp16 33-64-row decode kernel
+    # the prefill kernel (above 64 rows) and the fp16 17-64-row decode kernel
     # round w_eff*s to the activation dtype before multiplying
     extra = graded_rounding_bound(x, W, s, t, max_bits, dtype) if rounds_weight(M, dtype) else None
     assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, max_bits, 128, dtype), dtype, what=f"union M={M}",
@@ -393,12 +393,12 @@ def test_split_k_counters_return_to_zero():
 
 
 @pytest.mark.parametrize("mode", ["union", "dense"])
-@pytest.mark.parametrize("M", [40, 64, 130])
+@pytest.mark.parametrize("M", [20, 40, 64, 130])
 def test_large_scales_round_once(M, mode):
     """Scales of +-200 in one group next to ordinary ones (|w*s| up to ~2.6e4,
     near the fp16 range of the rounded weight) still give the oracle's product
     within the weight-rounding bound, on the fp16 kernels that round w*s to
-    fp16 (33-64-row decode, prefill) in both grading modes."""
+    fp16 (17-64-row decode, prefill) in both grading modes."""
     from grinqh.kernel import grinqh_gemv_batch_union, grinqh_prefill_dense
     rng = np.random.default_rng(500 + M)
     K, N, b, dtype = 512, 768, 8, "float16"
@@ -424,7 +424,7 @@ def test_large_scales_round_once(M, mode):
     assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}", extra_tol=extra)
 
 
-@pytest.mark.parametrize("M", [1, 3, 20])
+@pytest.mark.parametrize("M", [1, 3, 20, 40, 64, 100])
 def test_nonfinite_rows_poison_their_output_row(M):
     """A NaN or inf activation makes its whole output row NaN, as the
     reference's sum of beta*x (0*NaN, 0*inf) does (grinqh/kernel.py:113-114)."""

@@ -45,7 +45,7 @@ namespace grinqh {
 
 constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged in LDS)
 
-// 33-64 rows in fp16 ("scaled" path) multiply the scaled weight RNE(w * s),
+// 17-64 rows in fp16 ("scaled" path) multiply the scaled weight RNE(w * s),
 // built in registers as the prefill builds it in LDS, and accumulate the
 // output directly: no per-group partial sums, no correction column, no group
 // epilogue.  The registers this frees let a wave cover two output dwords of all
@@ -54,9 +54,9 @@ constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged
 // waves instead of four.  The weight is rounded once to fp16, as in the
 // reference's dense path (grinqh/kernel.py:586).
 template <typename DT, int MT>
-constexpr bool decode_scaled() { return MT == 4 && DT::id == F16::id; }
+constexpr bool decode_scaled() { return MT >= 2 && DT::id == F16::id; }
 template <typename DT, int MT>
-constexpr int decode_waves() { return decode_scaled<DT, MT>() ? 8 : 4; }
+constexpr int decode_waves() { return (decode_scaled<DT, MT>() || MT == 1) ? 8 : 4; }
 
 template <typename DT, int MT, int Z, bool DENSE>
 __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kernel(DecodeParams p) {
@@ -64,13 +64,13 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   constexpr int NWV = decode_waves<DT, MT>();
   constexpr int NT = 64 * NWV;         // threads per block
   constexpr int MP = 16 * MT;          // padded rows of x
-  constexpr int NJ = SC ? 2 : 4 / MT;  // output dwords j per wave
-  constexpr int KW = SC ? 4 : 4 / MT;  // K sub-ranges per block
+  constexpr int NJ = NWV == 8 ? 2 : 4 / MT;  // output dwords j per wave
+  constexpr int KW = NWV == 8 ? 4 : 4 / MT;  // K sub-ranges per block
   constexpr int JG = NWV / KW;         // groups of output dwords (waves per K sub-range)
   // tiles of loads in flight ahead of the one unpacked; the scaled path runs
   // two waves per SIMD on 256 registers, with one tile ahead and its A operand
   // loaded when the tile starts
-  constexpr int PF = SC ? 1 : 2;
+  constexpr int PF = (SC && MT == 4) ? 1 : 2;
   constexpr bool A_LATE = SC;
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
@@ -132,7 +132,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
 #pragma unroll
     for (int k = 0; k < XPT; ++k) {
       if constexpr (AG) break;
-      const int m = mb + k * (256 / CPR);
+      const int m = mb + k * (NT / CPR);
       const uint32_t off =
           (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
       xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
@@ -152,7 +152,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     if constexpr (!AG) {
 #pragma unroll
       for (int k = 0; k < XPT; ++k) {
-        const int m = mb + k * (256 / CPR);
+        const int m = mb + k * (NT / CPR);
         *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
       }
     }
@@ -438,6 +438,19 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
         }
       }
     }
+  }
+
+  // the scaled path multiplies w_eff * s directly: graded rows with a
+  // non-finite activation become NaN, as in the reference
+  if constexpr (SC && !DENSE) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) Y[mt][jj][b][e] = graded_nonfinite_to_nan(Y[mt][jj][b][e]);
   }
 
   // ---- phase 4: output (direct, or split-K partials + last-block reduction)

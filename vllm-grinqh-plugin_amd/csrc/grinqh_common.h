@@ -66,6 +66,17 @@ __device__ __forceinline__ uint16_t finish_output(float acc, const uint16_t* bia
   return y;
 }
 
+// Graded (union) products that multiply the scaled weight w_eff * s directly:
+// a sum that is not finite can only come from a non-finite activation in its
+// row (fp16/bf16 products cannot overflow fp32), and every output of such a
+// row is then non-finite.  The reference keeps the midpoint-bias term apart,
+// sum_k beta_k * x_k * s (grinqh/kernel.py:113-114, 148-158), whose 0 * inf or
+// 0 * NaN makes the whole row NaN; mapping each non-finite sum to NaN gives
+// that row.
+__device__ __forceinline__ float graded_nonfinite_to_nan(float v) {
+  return __builtin_isfinite(v) ? v : __builtin_nanf("");
+}
+
 // ---------------------------------------------------------------- bytes
 
 // v_perm_b32: byte selector 0..3 picks from `lo`, 4..7 from `hi`, 0x0c gives 0.

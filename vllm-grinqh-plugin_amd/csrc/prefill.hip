@@ -256,10 +256,11 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + wm * WM + 16 * i + 4 * q + e;
         if (m >= p.M) continue;
+        const float v = DENSE ? acc[i][r][e] : graded_nonfinite_to_nan(acc[i][r][e]);
         if (p.splits == 1)
-          p.y[(int64_t)m * p.N + n] = finish_output<DT>(acc[i][r][e], p.bias, (int)n);
+          p.y[(int64_t)m * p.N + n] = finish_output<DT>(v, p.bias, (int)n);
         else
-          p.partial[((int64_t)blockIdx.z * p.M + m) * p.N + n] = acc[i][r][e];
+          p.partial[((int64_t)blockIdx.z * p.M + m) * p.N + n] = v;
       }
     }
 }
