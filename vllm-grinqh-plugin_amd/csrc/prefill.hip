@@ -311,15 +311,15 @@ int prefill_splits(int64_t M, int64_t K, int64_t N) {
 // stage), else 32-row stages.
 template <typename DT>
 static int launch_prefill_dt(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
-  // 256-row tiles: one wave per SIMD (128 x 128 per wave); 128-row tiles: two
-  // waves per SIMD (32 x 128 per wave), whose dequantization and MFMAs overlap.
+  // 256-row tiles: 8 waves, two per SIMD (64 x 128 per wave), 32-row stages
+  // (64-row stages do not fit 256 registers); 128-row tiles: 8 waves (32 x 128
+  // per wave).  Two waves per SIMD let one wave's dequantization and loads
+  // overlap the other's MFMAs.
   const bool bk64 = (p.K % 64 == 0) && (p.gs % 64 == 0);
   // (bf16's fp32 dequantization does not fit the 256-row tile's registers:
   // it always takes 128-row tiles)
   if constexpr (DT::id == F16::id) {
-    if (prefill_block_rows(p.M, p.N) == 256)
-      return bk64 ? launch_prefill_bm<DT, 256, 4, 64>(p, Z, dense, st)
-                  : launch_prefill_bm<DT, 256, 4, 32>(p, Z, dense, st);
+    if (prefill_block_rows(p.M, p.N) == 256) return launch_prefill_bm<DT, 256, 8, 32>(p, Z, dense, st);
   }
   return bk64 ? launch_prefill_bm<DT, 128, 8, 64>(p, Z, dense, st)
               : launch_prefill_bm<DT, 128, 8, 32>(p, Z, dense, st);
