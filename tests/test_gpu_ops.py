@@ -392,6 +392,28 @@ def test_split_k_counters_return_to_zero():
                             what=f"M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [5, 20, 40, 64])
+@pytest.mark.parametrize("K", [32, 64, 96, 160, 416])
+def test_decode_short_k_ranges(K, M, dtype):
+    """K of 1-13 32-row tiles: the decode kernel's K sub-ranges (four per
+    block) are then partly or wholly empty, and the group size 32 puts a group
+    boundary at every tile."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(700 + K + M)
+    N, b, gs = 512, 8, 32
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)), dtype)
+    s = to_dtype_np(rng.standard_normal((K // gs, N)), dtype)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), None, b, gs, N // 4, t)
+    pre = O.gemv_union_f64(x, W, s, t, b, gs)
+    extra = graded_rounding_bound(x, W, s, t, b, dtype, group_size=gs) if rounds_weight(M, dtype) else None
+    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, b, gs, dtype), dtype, what=f"K={K} M={M}",
+                        extra_tol=extra)
+
+
 @pytest.mark.parametrize("mode", ["union", "dense"])
 @pytest.mark.parametrize("M", [20, 40, 64, 130])
 def test_large_scales_round_once(M, mode):
