@@ -211,16 +211,10 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
     for (int r = 0; r < 8; ++r) acc[i][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  fetch_order(s_begin);
-  load_stage(s_begin);
-  store_stage(0);
-  __syncthreads();
-  for (int s = s_begin; s < s_end; ++s) {
-    const int buf = (s - s_begin) & 1;
-    if (s + 1 < s_end) load_stage(s + 1);
-    // All fragments of a 32-deep k step are read before its MFMAs, and the
-    // next k step's fragments are read while they run, so the matrix core is
-    // not left waiting on LDS between tiles.
+  // MFMAs of one stage from LDS buffer buf.  All fragments of a 32-deep k step
+  // are read before its MFMAs, and the next k step's fragments are read while
+  // they run, so the matrix core is not left waiting on LDS between tiles.
+  auto multiply_stage = [&](int buf) {
     u32x4_t Bf[2][8], Af[2][MTW];
     auto read_frags = [&](int ks, int f) {
 #pragma unroll
@@ -240,9 +234,25 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int r = 0; r < 8; ++r) acc[i][r] = mfma16x16x32<DT>(Af[ks & 1][i], Bf[ks & 1][r], acc[i][r]);
     }
-    if (s + 1 < s_end) store_stage(buf ^ 1);
+  };
+
+  fetch_order(s_begin);
+  load_stage(s_begin);
+  store_stage(0);
+  __syncthreads();
+  // Every stage but the last loads and stores the next one, unconditionally:
+  // a loop body in which the loads are always consumed lets the compiler's
+  // wait counts stay exact (a conditional store made it wait for every
+  // outstanding load, scale loads included, at the top of each stage).
+  int s = s_begin;
+  for (; s + 1 < s_end; ++s) {
+    const int buf = (s - s_begin) & 1;
+    load_stage(s + 1);
+    multiply_stage(buf);
+    store_stage(buf ^ 1);
     __syncthreads();
   }
+  multiply_stage((s - s_begin) & 1);
 
   // epilogue: lane (c, q) holds rows 4q..4q+3 of each 16 x 16 tile
   const bool col_ok = (w0 + c) < p.NW;
