@@ -67,6 +67,11 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(p.planes), (short)0, (int)((uint64_t)p.K * (uint32_t)(Z * p.NW) * 4u), 0x00020000);
   const uint32_t plane_row_bytes = (uint32_t)(Z * p.NW) * 4u;
+  // scales through a buffer descriptor: the group's row offset is one scalar,
+  // this thread's column offset one register (no 64-bit address per scale)
+  const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.scale), (short)0, (int)((uint64_t)((p.K + p.gs - 1) / p.gs) * p.N * 2u), 0x00020000);
+  const uint32_t s_col_off = ((uint32_t)(4 * j0) * (uint32_t)p.NW + (uint32_t)wc_ld) * 2u;
 
   u32x4_t xa[AL];
   uint32_t D[RPT][Z];
@@ -95,7 +100,9 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     if (new_group) {  // this thread's columns: column tiles 4*j0 .., word column wc_ld
       const int g = k0 / p.gs;
 #pragma unroll
-      for (int r = 0; r < 4 * JPT; ++r) sraw[r] = p.scale[(int64_t)g * p.N + (int64_t)(4 * j0 + r) * p.NW + wc_ld];
+      for (int r = 0; r < 4 * JPT; ++r)
+        sraw[r] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, (int)(s_col_off + (uint32_t)r * (uint32_t)p.NW * 2u),
+                                                       (int)((uint32_t)g * (uint32_t)p.N * 2u), 0);
     }
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
