@@ -237,10 +237,11 @@ def test_union_graded_batches(M, max_bits, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("max_bits", BITS)
-@pytest.mark.parametrize("M,K,N", [(65, 256, 320), (300, 512, 768), (129, 96, 4112)])
+@pytest.mark.parametrize("M,K,N", [(65, 256, 320), (300, 512, 768), (129, 96, 4112), (100, 32, 256), (100, 64, 256),
+                                   (100, 128, 256)])
 def test_prefill_dense_shapes(M, K, N, max_bits, dtype):
     """Prefill kernel (more than 64 rows) against S9 with bias: partial row
-    tiles, column blocks cut short (N/16 not a multiple of 16), K of 3 stages."""
+    tiles, column blocks cut short (N/16 not a multiple of 16), K of 1-4 stages."""
     from grinqh.kernel import run_product
     rng = np.random.default_rng(M + K + N + max_bits)
     W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)

@@ -31,7 +31,7 @@ namespace grinqh {
 // loads are issued before the previous stage's MFMAs and consumed after them,
 // so a longer stage hides more load latency.  Each dequantizing thread owns one
 // word column, BK/16 rows and 4*JPT column tiles.
-template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC>
+template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC, int PD>
 __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams p) {
   constexpr int NT = WAVES * 64;
   constexpr int SH = 8 - 2 * Z;
@@ -73,11 +73,14 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       const_cast<uint16_t*>(p.scale), (short)0, (int)((uint64_t)((p.K + p.gs - 1) / p.gs) * p.N * 2u), 0x00020000);
   const uint32_t s_col_off = ((uint32_t)(4 * j0) * (uint32_t)p.NW + (uint32_t)wc_ld) * 2u;
 
-  u32x4_t xa[AL];
-  uint32_t D[RPT][Z];
-  float sig[RPT];
-  uint16_t sraw[4 * JPT];  // scales of the stage's group when it starts a new group
-  bool new_group = false;
+  // registers of one stage's global loads; PD stages are in flight at once
+  struct Slot {
+    u32x4_t xa[AL];
+    uint32_t D[RPT][Z];
+    float sig[RPT];
+    uint16_t sraw[4 * JPT];  // scales of the stage's group when it starts a new group
+    bool new_group;
+  };
   // Grade-grouped order (graded batches, p.perm set): the weight rows of a
   // stage come from perm, and planes outside the union of their zone sets are
   // not fetched (past-the-end offsets read 0).  The order of stage s+1 is
@@ -94,14 +97,14 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       if (BK == 64) planes_nx |= p.stage_bits[(k0 >> 5) + 1];
     }
   };
-  auto load_stage = [&](int s) {
+  auto load_stage = [&](int s, Slot& L) {
     const int k0 = s * BK;
-    new_group = (s == s_begin) || (k0 / p.gs != (k0 - BK) / p.gs);
-    if (new_group) {  // this thread's columns: column tiles 4*j0 .., word column wc_ld
+    L.new_group = (s == s_begin) || (k0 / p.gs != (k0 - BK) / p.gs);
+    if (L.new_group) {  // this thread's columns: column tiles 4*j0 .., word column wc_ld
       const int g = k0 / p.gs;
 #pragma unroll
       for (int r = 0; r < 4 * JPT; ++r)
-        sraw[r] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, (int)(s_col_off + (uint32_t)r * (uint32_t)p.NW * 2u),
+        L.sraw[r] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, (int)(s_col_off + (uint32_t)r * (uint32_t)p.NW * 2u),
                                                        (int)((uint32_t)g * (uint32_t)p.N * 2u), 0);
     }
 #pragma unroll
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
       const int m = m0 + row;
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + k0 + 8 * piece) * 2) : 0x80000000u;
-      xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+      L.xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
     if constexpr (DENSE) {
 #pragma unroll
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
         const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
 #pragma unroll
         for (int z = 0; z < Z; ++z)
-          D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
+          L.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
       }
     } else {
       const bool grouped = p.perm != nullptr;
@@ -130,9 +133,9 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int z = 0; z < Z; ++z) {
           const uint32_t off = ((planes >> z) & 1u) ? rb + (uint32_t)z * p.NW * 4u : 0x80000000u;
-          D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)off, 0, 0);
+          L.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)off, 0, 0);
         }
-        sig[e] = p.sigma[row];
+        L.sig[e] = p.sigma[row];
       }
       fetch_order(s + 1);
     }
@@ -143,32 +146,32 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 
   // x rows as they are; B: grade (union), rebuild code bytes, RNE(w * s),
   // written as (column tile, column)[k]
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&](int buf, Slot& L) {
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
       const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
-      *reinterpret_cast<u32x4_t*>(&s_a[buf][row * KP + 8 * piece]) = xa[i];
+      *reinterpret_cast<u32x4_t*>(&s_a[buf][row * KP + 8 * piece]) = L.xa[i];
     }
     int beta[RPT];
 #pragma unroll
     for (int e = 0; e < RPT; ++e) {
-      const uint32_t bits = DENSE ? ((1u << Z) - 1u) : zone_bits<Z>(sig[e], p.thr.t);
+      const uint32_t bits = DENSE ? ((1u << Z) - 1u) : zone_bits<Z>(L.sig[e], p.thr.t);
       beta[e] = DENSE ? 0 : midpoint_bias<Z>(bits);
       if (!DENSE) {
 #pragma unroll
-        for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((bits >> z) & 1u);
+        for (int z = 0; z < Z; ++z) L.D[e][z] &= 0u - ((bits >> z) & 1u);
       }
-      D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U & mask) + 128
+      L.D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U & mask) + 128
 #pragma unroll
-      for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
+      for (int z = 1; z < Z; ++z) L.D[e][z] = rotr(L.D[e][z], (uint32_t)(2 * z));
     }
-    if (new_group) {
+    if (L.new_group) {
 #pragma unroll
       for (int r = 0; r < 4 * JPT; ++r) {
         if constexpr (DT::id == F16::id)
-          s2[r] = (uint32_t)sraw[r] | ((uint32_t)sraw[r] << 16);
+          s2[r] = (uint32_t)L.sraw[r] | ((uint32_t)L.sraw[r] << 16);
         else
-          sf[r] = to_f32<DT>(sraw[r]) * (1.0f / (float)(1 << SH));
+          sf[r] = to_f32<DT>(L.sraw[r]) * (1.0f / (float)(1 << SH));
       }
     }
 #pragma unroll
@@ -191,10 +194,10 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const int ee = 2 * pp + e;
-          uint32_t h = (Z == 4) ? D[ee][3] : (D[ee][0] & (0x03030303u << (2 * ((3 - j) & 3))));
+          uint32_t h = (Z == 4) ? L.D[ee][3] : (L.D[ee][0] & (0x03030303u << (2 * ((3 - j) & 3))));
 #pragma unroll
           for (int z = (Z == 4 ? 0 : 1); z < (Z == 4 ? 3 : Z); ++z)
-            h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), D[ee][z], h);
+            h = bfi(0x03030303u << (2 * ((3 - z - j) & 3)), L.D[ee][z], h);
           V[e] = rotr(h, (uint32_t)(32 - 2 * j) & 31u);
         }
 #pragma unroll
@@ -243,23 +246,60 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     }
   };
 
+  // The loop bodies below load and store unconditionally: with the loads
+  // always consumed inside the body the compiler's wait counts stay exact (a
+  // conditional store made it wait for every outstanding load, scale loads
+  // included, at the top of each stage).  Stage t is multiplied from LDS
+  // buffer (t - s_begin) & 1.
+  Slot LA, LB;
   fetch_order(s_begin);
-  load_stage(s_begin);
-  store_stage(0);
-  __syncthreads();
-  // Every stage but the last loads and stores the next one, unconditionally:
-  // a loop body in which the loads are always consumed lets the compiler's
-  // wait counts stay exact (a conditional store made it wait for every
-  // outstanding load, scale loads included, at the top of each stage).
+  load_stage(s_begin, LA);
+  store_stage(0, LA);
   int s = s_begin;
-  for (; s + 1 < s_end; ++s) {
-    const int buf = (s - s_begin) & 1;
-    load_stage(s + 1);
-    multiply_stage(buf);
-    store_stage(buf ^ 1);
+  if constexpr (PD == 1) {
     __syncthreads();
+    for (; s + 1 < s_end; ++s) {  // stage s+1 loads while stage s is multiplied
+      const int buf = (s - s_begin) & 1;
+      load_stage(s + 1, LA);
+      multiply_stage(buf);
+      store_stage(buf ^ 1, LA);
+      __syncthreads();
+    }
+    multiply_stage((s - s_begin) & 1);
+  } else {
+    // two stages in flight: at the top of each iteration stage s is in LDS
+    // buffer 0 and stage s+1 is loading into LB (a single-stage range loads
+    // its stage twice, harmlessly)
+    load_stage(s + 1 < s_end ? s + 1 : s, LB);
+    __syncthreads();
+    for (; s + 3 < s_end; s += 2) {
+      load_stage(s + 2, LA);
+      multiply_stage(0);
+      store_stage(1, LB);
+      __syncthreads();
+      load_stage(s + 3, LB);
+      multiply_stage(1);
+      store_stage(0, LA);
+      __syncthreads();
+    }
+    if (s + 2 < s_end) {  // stages s, s+1, s+2 left
+      load_stage(s + 2, LA);
+      multiply_stage(0);
+      store_stage(1, LB);
+      __syncthreads();
+      multiply_stage(1);
+      store_stage(0, LA);
+      __syncthreads();
+      multiply_stage(0);
+    } else if (s + 1 < s_end) {  // stages s, s+1 left
+      multiply_stage(0);
+      store_stage(1, LB);
+      __syncthreads();
+      multiply_stage(1);
+    } else {
+      multiply_stage(0);
+    }
   }
-  multiply_stage((s - s_begin) & 1);
 
   // epilogue: lane (c, q) holds rows 4q..4q+3 of each 16 x 16 tile
   const bool col_ok = (w0 + c) < p.NW;
@@ -282,7 +322,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     }
 }
 
-template <typename DT, int BM, int Z, int WAVES, int BK, int OCC>
+template <typename DT, int BM, int Z, int WAVES, int BK, int PD>
 static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st) {
   PrefillParams p = p0;  // K ranges of whole BK stages, none empty
   const int nst = p.K / BK;
@@ -290,18 +330,18 @@ static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st
   p.splits = (nst + p.stages_per_split - 1) / p.stages_per_split;
   const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM, p.splits);
   if (dense)
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK, OCC>), grid, dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK, 1, PD>), grid, dim3(WAVES * 64), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK, OCC>), grid, dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK, 1, PD>), grid, dim3(WAVES * 64), 0, st, p);
 }
 
-template <typename DT, int BM, int WAVES, int BK, int OCC = 1>
+template <typename DT, int BM, int WAVES, int BK, int PD>
 static int launch_prefill_bm(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
   switch (Z) {
-    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK, OCC>(p, dense, st); break;
-    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK, OCC>(p, dense, st); break;
-    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK, OCC>(p, dense, st); break;
-    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK, OCC>(p, dense, st); break;
+    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK, PD>(p, dense, st); break;
+    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK, PD>(p, dense, st); break;
+    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK, PD>(p, dense, st); break;
+    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK, PD>(p, dense, st); break;
     default: return GRINQH_ERR_INVALID;
   }
   return GRINQH_OK;
@@ -324,28 +364,38 @@ int prefill_splits(int64_t M, int64_t K, int64_t N) {
   return splits > 1 ? (int)splits : 1;
 }
 
-// 64-row stages when K and the group size allow (more load latency hidden per
-// stage), else 32-row stages.
-template <typename DT>
-static int launch_prefill_dt(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
-  // 256-row tiles: 8 waves, two per SIMD (64 x 128 per wave), 32-row stages
-  // (64-row stages do not fit 256 registers); 128-row tiles: 8 waves (32 x 128
-  // per wave).  Two waves per SIMD let one wave's dequantization and loads
-  // overlap the other's MFMAs.
+// Stage rows and stages in flight per configuration.  256-row tiles (fp16,
+// grid of at least one block per CU): 8 waves, two per SIMD (64 x 128 per
+// wave), 32-row stages, one stage in flight (64-row stages or a second stage
+// do not fit 256 registers).  128-row tiles: 8 waves (32 x 128 per wave); fp16
+// dense batches run 32-row stages with two stages in flight, the others
+// 64-row stages (when K and the group size allow) with one.  Two waves per
+// SIMD let one wave's dequantization and loads overlap the other's MFMAs.
+struct PrefillShape {
+  int bm, bk, pd;
+};
+static PrefillShape prefill_shape(const PrefillParams& p, int dtype, bool dense) {
   const bool bk64 = (p.K % 64 == 0) && (p.gs % 64 == 0);
   // (bf16's fp32 dequantization does not fit the 256-row tile's registers:
   // it always takes 128-row tiles)
-  if constexpr (DT::id == F16::id) {
-    if (prefill_block_rows(p.M, p.N) == 256) return launch_prefill_bm<DT, 256, 8, 32>(p, Z, dense, st);
+  if (dtype == GRINQH_DTYPE_F16 && prefill_block_rows(p.M, p.N) == 256) return {256, 32, 1};
+  if (dtype == GRINQH_DTYPE_F16 && dense) return {128, 32, 2};
+  return {128, bk64 ? 64 : 32, 1};
+}
+
+template <typename DT>
+static int launch_prefill_dt(const PrefillParams& p, const PrefillShape& sh, int Z, bool dense, hipStream_t st) {
+  if constexpr (DT::id == F16::id) {  // the shapes only fp16 takes
+    if (sh.bm == 256) return launch_prefill_bm<DT, 256, 8, 32, 1>(p, Z, dense, st);
+    if (sh.pd == 2) return launch_prefill_bm<DT, 128, 8, 32, 2>(p, Z, dense, st);
   }
-  return bk64 ? launch_prefill_bm<DT, 128, 8, 64>(p, Z, dense, st)
-              : launch_prefill_bm<DT, 128, 8, 32>(p, Z, dense, st);
+  return sh.bk == 64 ? launch_prefill_bm<DT, 128, 8, 64, 1>(p, Z, dense, st)
+                     : launch_prefill_bm<DT, 128, 8, 32, 1>(p, Z, dense, st);
 }
 
 // K ranges launch_prefill_t runs for an upper bound `splits` (whole stages).
-static int prefill_splits_run(const PrefillParams& p, int splits) {
-  const int BK = ((p.K % 64 == 0) && (p.gs % 64 == 0)) ? 64 : 32;
-  const int nst = p.K / BK;
+static int prefill_splits_run(const PrefillParams& p, int splits, int bk) {
+  const int nst = p.K / bk;
   const int sps = (nst + splits - 1) / splits;
   return (nst + sps - 1) / sps;
 }
@@ -354,10 +404,11 @@ int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, 
                    int* splits_run) {
   if (!dense && p.sigma == nullptr) return GRINQH_ERR_INVALID;
   if (p.splits < 1 || (p.splits > 1 && p.partial == nullptr)) return GRINQH_ERR_INVALID;
-  *splits_run = prefill_splits_run(p, p.splits);
+  const PrefillShape sh = prefill_shape(p, dtype, dense);
+  *splits_run = prefill_splits_run(p, p.splits, sh.bk);
   const int Z = max_bits / 2;
-  const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_prefill_dt<BF16>(p, Z, dense, st)
-                                            : launch_prefill_dt<F16>(p, Z, dense, st);
+  const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_prefill_dt<BF16>(p, sh, Z, dense, st)
+                                            : launch_prefill_dt<F16>(p, sh, Z, dense, st);
   if (rc != GRINQH_OK) return rc;
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
