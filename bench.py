@@ -261,9 +261,10 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"step {ms_per_step * 1e3:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s)")
 
-    # ---------------- kernel timing: HIP events recorded by the library right
-    # around each product's main kernel (before its split-K reduction), on the
-    # stream the kernel runs on
+    # ---------------- kernel timing: HIP events that the dispatch of each
+    # product's main kernel records as the kernel starts and ends (the
+    # library launches it with hipExtLaunchKernelGGL), on the stream the
+    # kernel runs on: its execution alone, without the split-K reduction
     lib = _lib.load_library()
     ev_pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 for _ in range(args.reps)]

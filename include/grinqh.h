@@ -119,12 +119,13 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
                          void* stream);
 
 /* Benchmark instrumentation; no counterpart in the reference.  Arms a one-shot
- * timer: the next grinqh_gemm_or_gemv / grinqh_gemv_batch_union /
- * grinqh_prefill_dense call (from any thread) records `event_before` on its
- * stream immediately before its first main kernel and `event_after` right
- * after it, before any split-K reduction kernel, so the events bracket that
- * kernel alone.  Both are hipEvent_t handles created by the caller; passing
- * two NULLs disarms.  Not for use under graph capture. */
+ * timer: in the next grinqh_gemm_or_gemv / grinqh_gemv_batch_union /
+ * grinqh_prefill_dense call (from any thread), the dispatch of its first main
+ * kernel records `event_before` as the kernel starts and `event_after` as it
+ * ends (hipExtLaunchKernelGGL), so the events time that kernel's execution
+ * alone: no split-K reduction, no event or dispatch overhead.  Both are
+ * hipEvent_t handles created by the caller with timing enabled; passing two
+ * NULLs disarms.  Not for use under graph capture. */
 int grinqh_time_next_product(void* event_before, void* event_after);
 
 #ifdef __cplusplus

@@ -29,6 +29,23 @@ struct KernelEvents {
 };
 KernelEvents g_events;
 
+}  // namespace
+
+namespace grinqh {
+thread_local KernelTiming t_kernel_timing;
+}  // namespace grinqh
+
+namespace {
+
+// Hands an armed one-shot timer to this thread's next main-kernel launch.
+void arm_kernel_timing() {
+  std::lock_guard<std::mutex> lock(g_events.mu);
+  if (g_events.before != nullptr) {
+    t_kernel_timing = KernelTiming{g_events.before, g_events.after};
+    g_events.before = g_events.after = nullptr;
+  }
+}
+
 struct WorkspaceLayout {
   size_t counter_off, sigma_off, perm_off, stage_off, xsort_off, partial_off, total;
   DecodePlan plan;
@@ -121,19 +138,11 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     p.x = xsorted;
     p.ldx = d.K;
   }
-  hipEvent_t ev_after = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_events.mu);
-    if (g_events.before != nullptr) {
-      if (hipEventRecord(g_events.before, st) != hipSuccess) return GRINQH_ERR_HIP;
-      ev_after = g_events.after;
-      g_events.before = g_events.after = nullptr;
-    }
-  }
+  arm_kernel_timing();
   int splits_run = 1;
   int rc = launch_prefill(p, max_bits, dtype, !graded, st, &splits_run);
+  t_kernel_timing = KernelTiming{};
   if (rc != GRINQH_OK) return rc;
-  if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
   if (splits_run > 1) {  // add the K ranges in order, cast, bias
     DecodeParams r = d;
     r.M = (int)M;
@@ -194,18 +203,10 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
     const int64_t block_cols = mc <= kGemvMaxRows ? 1024 : 256;  // logical columns per column block
     p.counters =
         splitk_in_kernel(plan, mc, N, block_cols) ? reinterpret_cast<uint32_t*>(ws + wl.counter_off) : nullptr;
-    hipEvent_t ev_after = nullptr;
-    if (m0 == 0) {
-      std::lock_guard<std::mutex> lock(g_events.mu);
-      if (g_events.before != nullptr) {
-        if (hipEventRecord(g_events.before, st) != hipSuccess) return GRINQH_ERR_HIP;
-        ev_after = g_events.after;
-        g_events.before = g_events.after = nullptr;
-      }
-    }
+    if (m0 == 0) arm_kernel_timing();
     rc = launch_main(p, plan, max_bits, dtype, !graded, st);
+    t_kernel_timing = KernelTiming{};
     if (rc != GRINQH_OK) return rc;
-    if (ev_after != nullptr && hipEventRecord(ev_after, st) != hipSuccess) return GRINQH_ERR_HIP;
     if (plan.splits > 1 && p.counters == nullptr) {
       rc = launch_splitk_reduce(p, plan.splits, dtype, st);
       if (rc != GRINQH_OK) return rc;

@@ -604,9 +604,9 @@ static void launch_decode_t(const DecodeParams& p, const DecodePlan& pl, bool de
   const dim3 grid(pl.col_blocks * pl.splits);
   const dim3 block(64 * decode_waves<DT, MT>());
   if (dense)
-    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, true>), grid, block, 0, st, p);
+    launch_main_kernel(decode_kernel<DT, MT, Z, true>, grid, block, st, p);
   else
-    hipLaunchKernelGGL((decode_kernel<DT, MT, Z, false>), grid, block, 0, st, p);
+    launch_main_kernel(decode_kernel<DT, MT, Z, false>, grid, block, st, p);
 }
 
 template <typename DT, int MT>

@@ -368,9 +368,9 @@ template <typename DT, int MR, int Z>
 static void launch_gemv_t(const DecodeParams& p, const DecodePlan& pl, bool dense, hipStream_t st) {
   const dim3 grid(pl.col_blocks, pl.splits);
   if (dense)
-    hipLaunchKernelGGL((gemv_kernel<DT, MR, Z, true>), grid, dim3(256), 0, st, p);
+    launch_main_kernel(gemv_kernel<DT, MR, Z, true>, grid, dim3(256), st, p);
   else
-    hipLaunchKernelGGL((gemv_kernel<DT, MR, Z, false>), grid, dim3(256), 0, st, p);
+    launch_main_kernel(gemv_kernel<DT, MR, Z, false>, grid, dim3(256), st, p);
 }
 
 template <typename DT, int MR>

@@ -1,5 +1,6 @@
 // Internal launch interface between the C ABI (capi.hip) and the kernel files.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -112,6 +113,28 @@ int launch_grade_order(const float* sigma, const GradeThresholds& thr, int K, in
                        uint32_t* stage_bits, hipStream_t st);
 int launch_permute_cols(const uint16_t* x, int64_t ldx, const int* perm, int M, int K, uint16_t* xs,
                         hipStream_t st);
+
+// Benchmark timing of a product's main kernel: when armed (by
+// grinqh_time_next_product, for the calling thread's next product), the next
+// main-kernel launch on this thread hands the two events to the dispatch
+// itself (hipExtLaunchKernelGGL), which records them as the kernel starts and
+// ends: their interval is the kernel's execution alone, without the event and
+// dispatch overhead that records around the launch would add.
+struct KernelTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local KernelTiming t_kernel_timing;
+
+template <typename P>
+inline void launch_main_kernel(void (*kernel)(P), dim3 grid, dim3 block, hipStream_t st, const P& p) {
+  KernelTiming& kt = t_kernel_timing;
+  if (kt.start != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, kt.start, kt.stop, 0, p);
+    kt = KernelTiming{};
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, p);
+  }
+}
 
 int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);
 int launch_prepare_weight(const int8_t* W, uint32_t* out, int K, int N, int max_bits, hipStream_t st);

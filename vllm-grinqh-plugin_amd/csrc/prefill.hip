@@ -330,9 +330,9 @@ static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st
   p.splits = (nst + p.stages_per_split - 1) / p.stages_per_split;
   const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM, p.splits);
   if (dense)
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, true, WAVES, BK, 1, PD>), grid, dim3(WAVES * 64), 0, st, p);
+    launch_main_kernel(prefill_kernel<DT, BM, Z, true, WAVES, BK, 1, PD>, grid, dim3(WAVES * 64), st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DT, BM, Z, false, WAVES, BK, 1, PD>), grid, dim3(WAVES * 64), 0, st, p);
+    launch_main_kernel(prefill_kernel<DT, BM, Z, false, WAVES, BK, 1, PD>, grid, dim3(WAVES * 64), st, p);
 }
 
 template <typename DT, int BM, int WAVES, int BK, int PD>
