@@ -12,31 +12,37 @@
 //             column tiles r of 16 contiguous columns r*NW + w0 + c); two
 //             neighbours share every 128-byte line of the planes
 //   K range = `tiles_per_split` 32-row tiles (split-K)
-//   4 waves = MT groups of output dwords j x (4/MT) K sub-ranges
+//   waves   = groups of output dwords j x K sub-ranges: 8 waves (two per
+//             SIMD) as 2 dword pairs x 4 sub-ranges for 5-16 rows and for
+//             17-64 rows in fp16; 4 waves as MT dword groups x 4/MT
+//             sub-ranges for 17-64 rows in bf16
 //
-// Phase 1 (whole block): stage x[:, K range] in LDS, grade every row (sigma =
-// max_m |x|, zone bits, midpoint bias) and precompute each (row, plane) byte
-// offset, with bit 31 set for planes the row does not need.
+// Phase 1 (whole block): stage the scales (and, up to 16 rows, x[:, K range])
+// in LDS, grade every row (sigma = max_m |x|, zone bits, midpoint bias) and
+// precompute each (row, plane) byte offset, with bit 31 set for planes the
+// row does not need.
 //
 // Phase 2 (per wave): for each tile, each lane (c = lane&15, q = lane>>4) loads
 // one 32-bit plane word per (row, plane) of its 8 rows with raw buffer loads;
 // offsets with bit 31 set fall past the buffer end and return 0 without a
 // memory access, so only the planes a row needs are fetched and no load is
-// branched around.  Two tiles of loads stay in flight while the current tile
-// is unpacked (one wave per SIMD, 512 registers).  Code bytes are rebuilt
-// branch-free: G_z = rot(D_z, 2z), H_j = field merge of the G_z,
-// V_j = rot(H_j, -2j); then turned into the MFMA B operand:
-//   fp16: 0x64 | byte  -> 1024 + u exactly     (u = offset-binary code)
-//   bf16: cvt_f32_ubyte, upper half            -> u exactly
-// The constant offset and the midpoint bias beta are removed by one extra MFMA
-// per tile whose B operand is the per-row value beta*2^sh - off (a "correction
-// column" shared by all 16 columns); per scale group
-//   y += s[g][n] * 2^-sh * (C[m][n] + Cv[m])
-// in fp32, as grinqh/kernel.py:148-158 applies scales.
+// branched around.  One or two tiles of loads stay in flight while the
+// current tile is unpacked.  Code bytes are rebuilt branch-free:
+// G_z = rot(D_z, 2z), H_j = field merge of the G_z, V_j = rot(H_j, -2j); then
+// turned into the MFMA B operand in one of two ways:
+//   - code bytes (5-16 rows, and bf16): fp16 B = u as the subnormal u*2^-24
+//     (one v_perm per register), bf16 B = u; the offset 128 and the midpoint
+//     bias beta are removed by one extra MFMA per tile whose B operand is the
+//     per-row value beta*2^sh - 128 (a "correction column" shared by all 16
+//     columns), and per scale group y += s[g][n] * 2^-sh * (C[m][n] + Cv[m])
+//     in fp32, as grinqh/kernel.py:148-158 applies scales;
+//   - the scaled weight (17-64 rows in fp16): B = RNE(w_eff * s) in fp16,
+//     accumulated straight into y (no per-group sums, no correction column).
 //
-// Split-K partials are reduced deterministically: the 4/MT waves of a block
-// through LDS in fixed order; the K ranges (grid.y) by a second kernel that
-// adds the fp32 partials in range order and applies the output cast and bias.
+// Split-K partials are reduced deterministically: the K sub-ranges of a block
+// through LDS in fixed order; the K ranges of the grid either by the range
+// that finishes last (small reductions) or by a second kernel, both adding the
+// fp32 partials in range order before the output cast and bias.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 #include "splitk_complete.h"
