@@ -18,9 +18,12 @@
 // exactly the lane that holds them.
 //
 // Work decomposition
-//   grid.x = 64 word columns (1024 logical columns), grid.y = K range
-//   4 waves = 4 consecutive sub-ranges of the K range (8-row tiles), reduced
-//   through LDS in fixed order; K ranges are reduced by the split-K kernel.
+//   grid.x = 64 word columns (1024 logical columns), grid.y = K range; two
+//   blocks per CU
+//   4 waves = 4 consecutive sub-ranges of the K range (8-row tiles for one
+//   row, 4-row tiles on v_mfma_f32_16x16x16 for two to four), reduced through
+//   LDS in fixed order; the K ranges of the grid are added by the range that
+//   finishes last (small reductions) or by the split-K reduction kernel.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 #include "splitk_complete.h"

@@ -17,10 +17,10 @@
 // rounding bound of the dequantized weight.
 //
 // Tiles: a block computes BM rows x 256 logical columns (16 plane-word columns
-// x 16 column tiles); 4 waves as 2 x 2, each BM/2 rows x 8 column tiles.
-// Per 32-row stage: A (x) and the dequantized B go to the LDS buffer the MFMAs
-// are not reading, global loads for the following stage are in flight while
-// the current one is multiplied.
+// x 16 column tiles) with 8 waves, two per SIMD, as (BM/64 or 4) x 2.  Per
+// stage of BK rows of K: A (x) and the dequantized B go to the LDS buffer the
+// MFMAs are not reading, while the global loads of the next one or two
+// stages are in flight (register slots).
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 
@@ -28,9 +28,10 @@ namespace grinqh {
 
 // One block: BM rows x 256 logical columns; WAVES waves as (WAVES/2) x 2, each
 // BM/(WAVES/2) rows x 8 column tiles.  A stage is BK rows of K: its global
-// loads are issued before the previous stage's MFMAs and consumed after them,
-// so a longer stage hides more load latency.  Each dequantizing thread owns one
-// word column, BK/16 rows and 4*JPT column tiles.
+// loads are issued PD stages before its dequantization into LDS (PD register
+// slots), so they are in flight while the stages before it are multiplied.
+// Each dequantizing thread owns one word column, BK/16 rows and 4*JPT column
+// tiles.  OCC is the occupancy hint of the launch bounds.
 template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC, int PD>
 __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams p) {
   constexpr int NT = WAVES * 64;
