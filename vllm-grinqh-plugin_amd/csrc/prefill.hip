@@ -32,18 +32,23 @@ namespace grinqh {
 // slots), so they are in flight while the stages before it are multiplied.
 // Each dequantizing thread owns one word column, BK/16 rows and 4*JPT column
 // tiles.  OCC is the occupancy hint of the launch bounds.
-template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC, int PD>
+template <typename DT, int BM, int Z, bool DENSE, int WAVES, int BK, int OCC, int PD, bool WS = false>
 __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams p) {
   constexpr int NT = WAVES * 64;
+  // WS (warp-specialised): the first half of the waves only load and
+  // dequantize stages, the second half only multiply; each SIMD runs one of
+  // each, so one's VALU work overlaps the other's MFMAs
+  constexpr int NP = WS ? NT / 2 : NT;            // loading / dequantizing threads
   constexpr int SH = 8 - 2 * Z;
   constexpr int KP = BK + 8;        // halves per LDS row (padding: conflict-free fragment reads)
-  constexpr int WGM = WAVES / 2;    // waves along M (2 along N)
+  constexpr int WGM = WS ? 2 : WAVES / 2;  // multiplying waves along M (2 along N)
   constexpr int WM = BM / WGM;      // rows per wave
   constexpr int MTW = WM / 16;      // 16-row MFMA tiles per wave
   constexpr int CPR = BK / 8;       // 16-byte x chunks per row per stage
-  constexpr int AL = BM * CPR / NT;
+  constexpr int AL = BM * CPR / NP;
   constexpr int RPT = BK / 16;      // rows per dequantizing thread
-  constexpr int JPT = 4 * 256 / NT; // output dwords j per dequantizing thread
+  constexpr int JPT = 4 * 256 / NP; // output dwords j per dequantizing thread
+  static_assert(!WS || (WAVES == 8 && PD == 2), "warp-specialised shape");
   static_assert(MTW >= 1 && AL >= 1 && RPT % 2 == 0 && JPT >= 1, "tile shape");
 
   __shared__ __align__(16) uint16_t s_a[2][BM * KP];
@@ -51,7 +56,8 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % WGM, wn = wave / WGM;
+  const int cw = WS ? wave - NP / 64 : wave;  // index among the multiplying waves
+  const int wm = cw % WGM, wn = cw / WGM;
   const int c = lane & 15, q = lane >> 4;
   const int w0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * BM;
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     }
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
+      const int h = tid + NP * i, row = h / CPR, piece = h % CPR;
       const int m = m0 + row;
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + k0 + 8 * piece) * 2) : 0x80000000u;
       L.xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
@@ -150,7 +156,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   auto store_stage = [&](int buf, Slot& L) {
 #pragma unroll
     for (int i = 0; i < AL; ++i) {
-      const int h = tid + NT * i, row = h / CPR, piece = h % CPR;
+      const int h = tid + NP * i, row = h / CPR, piece = h % CPR;
       *reinterpret_cast<u32x4_t*>(&s_a[buf][row * KP + 8 * piece]) = L.xa[i];
     }
     int beta[RPT];
@@ -253,11 +259,46 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
   // included, at the top of each stage).  Stage t is multiplied from LDS
   // buffer (t - s_begin) & 1.
   Slot LA, LB;
-  fetch_order(s_begin);
-  load_stage(s_begin, LA);
-  store_stage(0, LA);
   int s = s_begin;
-  if constexpr (PD == 1) {
+  if constexpr (WS) {
+    // Both roles pass the same number of barriers: one after the first
+    // stage is stored, then one per stage but the last.  Stage t lives in
+    // LDS buffer (t - s_begin) & 1 and in register slot (t - s_begin) & 1
+    // (LA even, LB odd); two stages of loads are in flight.  Loads past the
+    // range repeat its last stage (unconditional loads keep the wait counts
+    // exact) and are never stored.
+    if (wave < NP / 64) {
+      const int last = s_end - 1;
+      fetch_order(s_begin);
+      load_stage(s_begin, LA);
+      store_stage(0, LA);
+      load_stage(min(s_begin + 1, last), LB);
+      load_stage(min(s_begin + 2, last), LA);
+      __syncthreads();
+      for (; s + 2 < s_end; s += 2) {  // store stages s+1 and s+2
+        store_stage(1, LB);
+        load_stage(min(s + 3, last), LB);
+        __syncthreads();
+        store_stage(0, LA);
+        load_stage(min(s + 4, last), LA);
+        __syncthreads();
+      }
+      if (s + 1 < s_end) {  // store stage s+1
+        store_stage(1, LB);
+        __syncthreads();
+      }
+      return;  // the multiplying waves write the output
+    }
+    __syncthreads();
+    for (; s + 1 < s_end; ++s) {
+      multiply_stage((s - s_begin) & 1);
+      __syncthreads();
+    }
+    multiply_stage((s - s_begin) & 1);
+  } else if constexpr (PD == 1) {
+    fetch_order(s_begin);
+    load_stage(s_begin, LA);
+    store_stage(0, LA);
     __syncthreads();
     for (; s + 1 < s_end; ++s) {  // stage s+1 loads while stage s is multiplied
       const int buf = (s - s_begin) & 1;
@@ -271,6 +312,9 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     // two stages in flight: at the top of each iteration stage s is in LDS
     // buffer 0 and stage s+1 is loading into LB (a single-stage range loads
     // its stage twice, harmlessly)
+    fetch_order(s_begin);
+    load_stage(s_begin, LA);
+    store_stage(0, LA);
     load_stage(s + 1 < s_end ? s + 1 : s, LB);
     __syncthreads();
     for (; s + 3 < s_end; s += 2) {
@@ -323,7 +367,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     }
 }
 
-template <typename DT, int BM, int Z, int WAVES, int BK, int PD>
+template <typename DT, int BM, int Z, int WAVES, int BK, int PD, bool WS>
 static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st) {
   PrefillParams p = p0;  // K ranges of whole BK stages, none empty
   const int nst = p.K / BK;
@@ -331,18 +375,18 @@ static void launch_prefill_t(const PrefillParams& p0, bool dense, hipStream_t st
   p.splits = (nst + p.stages_per_split - 1) / p.stages_per_split;
   const dim3 grid((p.NW + 15) / 16, (p.M + BM - 1) / BM, p.splits);
   if (dense)
-    launch_main_kernel(prefill_kernel<DT, BM, Z, true, WAVES, BK, 1, PD>, grid, dim3(WAVES * 64), st, p);
+    launch_main_kernel(prefill_kernel<DT, BM, Z, true, WAVES, BK, 1, PD, WS>, grid, dim3(WAVES * 64), st, p);
   else
-    launch_main_kernel(prefill_kernel<DT, BM, Z, false, WAVES, BK, 1, PD>, grid, dim3(WAVES * 64), st, p);
+    launch_main_kernel(prefill_kernel<DT, BM, Z, false, WAVES, BK, 1, PD, WS>, grid, dim3(WAVES * 64), st, p);
 }
 
-template <typename DT, int BM, int WAVES, int BK, int PD>
+template <typename DT, int BM, int WAVES, int BK, int PD, bool WS = false>
 static int launch_prefill_bm(const PrefillParams& p, int Z, bool dense, hipStream_t st) {
   switch (Z) {
-    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK, PD>(p, dense, st); break;
-    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK, PD>(p, dense, st); break;
-    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK, PD>(p, dense, st); break;
-    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK, PD>(p, dense, st); break;
+    case 1: launch_prefill_t<DT, BM, 1, WAVES, BK, PD, WS>(p, dense, st); break;
+    case 2: launch_prefill_t<DT, BM, 2, WAVES, BK, PD, WS>(p, dense, st); break;
+    case 3: launch_prefill_t<DT, BM, 3, WAVES, BK, PD, WS>(p, dense, st); break;
+    case 4: launch_prefill_t<DT, BM, 4, WAVES, BK, PD, WS>(p, dense, st); break;
     default: return GRINQH_ERR_INVALID;
   }
   return GRINQH_OK;
@@ -368,10 +412,12 @@ int prefill_splits(int64_t M, int64_t K, int64_t N) {
 // Stage rows and stages in flight per configuration.  256-row tiles (fp16,
 // grid of at least one block per CU): 8 waves, two per SIMD (64 x 128 per
 // wave), 32-row stages, one stage in flight (64-row stages or a second stage
-// do not fit 256 registers).  128-row tiles: 8 waves (32 x 128 per wave); fp16
-// dense batches run 32-row stages with two stages in flight, the others
-// 64-row stages (when K and the group size allow) with one.  Two waves per
-// SIMD let one wave's dequantization and loads overlap the other's MFMAs.
+// do not fit 256 registers).  128-row tiles: fp16 dense batches run the
+// warp-specialised form (4 waves load and dequantize 32-row stages with two
+// stages in flight, 4 waves of 64 x 128 multiply), the others 8 waves of
+// 32 x 128 with 64-row stages (when K and the group size allow) and one stage
+// in flight.  Two waves per SIMD let one wave's dequantization and loads
+// overlap the other's MFMAs.
 struct PrefillShape {
   int bm, bk, pd;
 };
@@ -388,7 +434,7 @@ template <typename DT>
 static int launch_prefill_dt(const PrefillParams& p, const PrefillShape& sh, int Z, bool dense, hipStream_t st) {
   if constexpr (DT::id == F16::id) {  // the shapes only fp16 takes
     if (sh.bm == 256) return launch_prefill_bm<DT, 256, 8, 32, 1>(p, Z, dense, st);
-    if (sh.pd == 2) return launch_prefill_bm<DT, 128, 8, 32, 2>(p, Z, dense, st);
+    if (sh.pd == 2) return launch_prefill_bm<DT, 128, 8, 32, 2, true>(p, Z, dense, st);
   }
   return sh.bk == 64 ? launch_prefill_bm<DT, 128, 8, 64, 1>(p, Z, dense, st)
                      : launch_prefill_bm<DT, 128, 8, 32, 1>(p, Z, dense, st);
