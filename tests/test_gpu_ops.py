@@ -301,16 +301,60 @@ def test_graded_prefill_grade_groups(t, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_256_row_tiles(dtype):
-    """Enough blocks for the 256-row tile variant (64 column blocks x 4 row
-    tiles; fp16 takes it, bf16 stays on 128-row tiles)."""
+    """Enough blocks for the fused kernel's 256-row tile variant (65 column
+    blocks x 4 row tiles; fp16 takes it, bf16 stays on 128-row tiles).  N / 16
+    is odd, so this batch size stays on the fused kernel rather than the
+    library-GEMM path."""
     from grinqh.kernel import grinqh_prefill_dense
-    M, K, N = 1000, 256, 16384
+    M, K, N = 1000, 256, 16400
     rng = np.random.default_rng(77)
     W, x, s = _setup(rng, K, N, 8, dtype, M=M)
     y = grinqh_prefill_dense(_tdt(x, dtype), _prepare(W, 8), _tdt(s, dtype), 128, N // 4, 8)
     pre = O.dense_prefill_f64(x, W, s, 128, dtype)
     assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="prefill 256-row tiles",
                         extra_tol=dense_rounding_bound(x, W, s, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", BITS)
+@pytest.mark.parametrize("M,K,N", [(512, 96, 256), (700, 512, 768), (512, 2080, 320), (600, 256, 4112)])
+def test_prefill_library_gemm(M, K, N, max_bits, dtype):
+    """Dense batches of 512 rows and more: the dense weight Wt[N][K] is written
+    once (dequant kernel: 64-row tiles, the last one partial when K % 64 ==
+    32; scale groups of 128 crossing tiles), then the library GEMM multiplies
+    it with the bias in its epilogue.  N / 16 not a multiple of 4 (4112) keeps
+    the fused kernel.  Held to S9 like the fused kernel."""
+    from grinqh.kernel import run_product
+    rng = np.random.default_rng(M * 7 + K + N + max_bits)
+    W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    y = run_product(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), _tdt(bias, dtype), max_bits, 128,
+                    N // 4, [0.0] * 4, "dense")
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, bias, 128, dtype), dtype, bias=bias,
+                        what=f"library prefill {M}x{K}x{N}", extra_tol=dense_rounding_bound(x, W, s, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_prefill_library_gemm_strided_rows(dtype):
+    """Library-GEMM prefill of activation rows with a leading dimension above
+    K (a column slice of a wider tensor), without bias, twice in a row on the
+    same workspace (the second call reuses the cached GEMM plan)."""
+    from grinqh.kernel import run_product
+    M, K, N, b = 520, 384, 512, 8
+    rng = np.random.default_rng(2024)
+    W, x, s = _setup(rng, K, N, b, dtype, M=M)
+    wide = np.concatenate([x, to_dtype_np(rng.standard_normal((M, 64)), dtype)], axis=1)
+    xt = _tdt(wide, dtype)[:, :K]
+    assert xt.stride(0) == K + 64
+    P = _prepare(W, b)
+    st = _tdt(s, dtype)
+    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+    fin = O.dense_prefill(x, W, s, None, 128, dtype)
+    for _ in range(2):
+        y = run_product(xt, P, st, None, b, 128, N // 4, [0.0] * 4, "dense")
+        assert_output_close(y, pre, fin, dtype, what="library prefill, strided rows",
+                            extra_tol=dense_rounding_bound(x, W, s, dtype))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -48,6 +48,8 @@ void arm_kernel_timing() {
 
 struct WorkspaceLayout {
   size_t counter_off, sigma_off, perm_off, stage_off, xsort_off, partial_off, total;
+  size_t wt_off, blas_off;  // library-GEMM prefill: dense weight [N][K], then the GEMM's workspace
+  bool library_gemm;
   DecodePlan plan;
 };
 
@@ -69,6 +71,13 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 // workspace shared by calls of different shapes keeps them zero.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
+  if (mode == GRINQH_MODE_DENSE && M >= kLibraryGemmRows && N % 64 == 0) {  // [counters | Wt | GEMM workspace]
+    w.library_gemm = true;
+    w.wt_off = kCounterBytes;
+    w.blas_off = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
+    w.total = w.blas_off + kLibraryGemmWorkspace;
+    return w;
+  }
   size_t partial = 0;
   if (M <= kDecodeMaxRows) {
     w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
@@ -107,6 +116,14 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // first reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
+  if (wl.library_gemm) {  // dense weight once, then the library GEMM
+    uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
+    arm_kernel_timing();
+    int rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, st);
+    t_kernel_timing = KernelTiming{};
+    if (rc != GRINQH_OK) return rc;
+    return gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
+  }
   PrefillParams p{};
   p.x = xs;
   p.ldx = d.ldx;
