@@ -336,6 +336,63 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("max_bits", [4, 8])
+@pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0], None],
+                         ids=["non_monotone", "skip_all", "all_planes", "tied", "quantiles"])
+def test_prefill_library_gemm_graded(t, max_bits, dtype):
+    """Graded (union) batches of 512 rows and more: the dequant kernel writes
+    RNE(w_eff * s) from each row's zone set (inactive planes not fetched,
+    midpoint bias added), then the library GEMM.  Zone sets that are not
+    prefixes, none, all, tied thresholds and the 70/20/8/2 % quantile mix, held
+    to S10 within the weight-rounding bound, with bias."""
+    from grinqh.kernel import run_product
+    M, K, N = 512, 1056, 512  # K % 64 == 32: the last dequant tile is half full
+    rng = np.random.default_rng(4321 + max_bits)
+    W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)
+    if t is None:
+        sigma = np.abs(x).max(0).astype(np.float32)
+        t = [0.0] + np.quantile(sigma, [0.7, 0.9, 0.98]).tolist()
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    y = run_product(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), _tdt(bias, dtype), max_bits, 128,
+                    N // 4, t, "union")
+    pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
+    assert_output_close(y, pre, O.gemv_union(x, W, s, bias, t, max_bits, 128, dtype), dtype, bias=bias,
+                        what=f"library graded prefill t={t}",
+                        extra_tol=graded_rounding_bound(x, W, s, t, max_bits, dtype))
+
+
+@pytest.mark.parametrize("mode", ["dense", "union"])
+def test_graph_capture_library_prefill(mode):
+    """A 512-row product (dequant kernel, library GEMM, graded row pass)
+    captured in a HIP graph and replayed several times with eager work in
+    between matches the eager result on every replay."""
+    from grinqh.kernel import run_product
+    M, K, N = 512, 2048, 1024
+    rng = np.random.default_rng(88)
+    W, x, s = _setup(rng, K, N, 8, "float16", M=M, scale_sd=0.01)
+    P, st = _prepare(W, 8), _tdt(s, "float16")
+    xin = _tdt(x, "float16")
+    t = [0.0, 0.5, 1.0, 2.0] if mode == "union" else [0.0] * 4
+    eager = run_product(xin, P, st, None, 8, 128, N // 4, t, mode).clone()
+    g = torch.cuda.CUDAGraph()
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        run_product(xin, P, st, None, 8, 128, N // 4, t, mode)  # sizes this stream's workspace
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s_cap):
+            yg = run_product(xin, P, st, None, 8, 128, N // 4, t, mode)
+    torch.cuda.current_stream().wait_stream(s_cap)
+    for i in range(4):
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, eager), f"replay {i}"
+        _ = run_product(xin, P, st, None, 8, 128, N // 4, t, mode)
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_library_gemm_strided_rows(dtype):
     """Library-GEMM prefill of activation rows with a leading dimension above
     K (a column slice of a wider tensor), without bias, twice in a row on the
@@ -491,19 +548,21 @@ def test_large_scales_round_once(M, mode):
     assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}", extra_tol=extra)
 
 
-@pytest.mark.parametrize("M", [1, 3, 20, 40, 64, 100])
-def test_nonfinite_rows_poison_their_output_row(M):
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [1, 3, 20, 40, 64, 100, 520])
+def test_nonfinite_rows_poison_their_output_row(M, dtype):
     """A NaN or inf activation makes its whole output row NaN, as the
-    reference's sum of beta*x (0*NaN, 0*inf) does (grinqh/kernel.py:113-114)."""
+    reference's sum of beta*x (0*NaN, 0*inf) does (grinqh/kernel.py:113-114).
+    520 rows take the library-GEMM path and its row pass."""
     rng = np.random.default_rng(6)
-    W, x, s = _setup(rng, 256, 256, 8, "float16", M=M)
+    W, x, s = _setup(rng, 256, 256, 8, dtype, M=M)
     x = x.copy()
     x[0, 17] = np.nan
     if M > 1:
         x[M - 1, 200] = np.inf
-    xt = _tdt(x, "float16")
+    xt = _tdt(x, dtype)
     from grinqh.kernel import grinqh_gemv_batch_union
-    y = grinqh_gemv_batch_union(xt, _prepare(W, 8), _tdt(s, "float16"), None, 8, 128, 64, [0.1, 0.5, 1.0, 2.0])
+    y = grinqh_gemv_batch_union(xt, _prepare(W, 8), _tdt(s, dtype), None, 8, 128, 64, [0.1, 0.5, 1.0, 2.0])
     y = y.float().cpu()
     assert torch.isnan(y[0]).all()
     if M > 1:

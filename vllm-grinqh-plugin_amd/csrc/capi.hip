@@ -71,9 +71,10 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 // workspace shared by calls of different shapes keeps them zero.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
-  if (mode == GRINQH_MODE_DENSE && M >= kLibraryGemmRows && N % 64 == 0) {  // [counters | Wt | GEMM workspace]
+  if (M >= kLibraryGemmRows && N % 64 == 0) {  // [counters | sigma (graded) | Wt | GEMM workspace]
     w.library_gemm = true;
-    w.wt_off = kCounterBytes;
+    w.sigma_off = kCounterBytes;
+    w.wt_off = w.sigma_off + (mode == GRINQH_MODE_UNION ? round_up((size_t)K * sizeof(float), 256) : 0);
     w.blas_off = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
     w.total = w.blas_off + kLibraryGemmWorkspace;
     return w;
@@ -116,13 +117,18 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // first reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
-  if (wl.library_gemm) {  // dense weight once, then the library GEMM
+  if (wl.library_gemm) {  // the (graded) weight once, then the library GEMM
     uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
-    arm_kernel_timing();
-    int rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, st);
-    t_kernel_timing = KernelTiming{};
+    float* sigma = graded ? reinterpret_cast<float*>(ws + wl.sigma_off) : nullptr;
+    int rc = graded ? launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st) : GRINQH_OK;
     if (rc != GRINQH_OK) return rc;
-    return gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
+    arm_kernel_timing();
+    rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, st);
+    t_kernel_timing = KernelTiming{};
+    if (rc == GRINQH_OK)
+      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
+    if (rc == GRINQH_OK && graded) rc = launch_nonfinite_rows_to_nan(xs, d.ldx, (int)M, d.K, ys, d.N, dtype, st);
+    return rc;
   }
   PrefillParams p{};
   p.x = xs;

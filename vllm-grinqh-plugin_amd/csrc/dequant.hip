@@ -1,6 +1,9 @@
 // Dense weight of a large prefill: Wt[n][k] = RNE(w[k][n] * s[k/gs][n]) in the
 // activation dtype, stored K-contiguous ([N][K]), for the library GEMM that
-// follows (blas.hip).
+// follows (blas.hip).  Graded (union) batches write RNE(w_eff * s) instead,
+// with each row's zone set from sigma_k = max_m |x[m][k]|: the planes of its
+// inactive zones are not fetched and its midpoint bias is added, as in the
+// fused prefill kernel.
 //
 // Replaces the dequantization half of grinqh_prefill_gemm_compiled
 // (grinqh/kernel.py:579-586: unpack_pyt + postshuffle + W * s, three torch
@@ -29,14 +32,16 @@ namespace {
 struct DequantParams {
   const uint32_t* planes;
   const uint16_t* scale;
-  uint16_t* wt;  // [N][K]
+  uint16_t* wt;        // [N][K]
+  const float* sigma;  // graded: union statistic [K]
+  GradeThresholds thr;
   int K, N, NW, gs;
 };
 
 constexpr int kDqColsPerBlock = 32;  // plane-word columns per block (4 waves x 8)
 constexpr int kDqRowsPerBlock = 64;  // rows of K per block
 
-template <typename DT, int Z>
+template <typename DT, int Z, bool DENSE>
 __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   constexpr int SH = 8 - 2 * Z;
   constexpr int LROW = 64 * Z + 4;  // words per word column in LDS (16-byte aligned rows)
@@ -50,7 +55,9 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
       const int seg = (threadIdx.x >> 3) + 32 * i;  // (k, z) of the block tile
       const int k = seg / Z, z = seg % Z;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-      if (kb + k < p.K && cb0 + 4 * pc < p.NW)
+      // graded: planes of inactive zones are not fetched (they read as zero)
+      const bool active = DENSE || (kb + k < p.K && ((zone_bits<Z>(p.sigma[kb + k], p.thr.t) >> z) & 1u));
+      if (kb + k < p.K && cb0 + 4 * pc < p.NW && active)
         v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.planes + (int64_t)(kb + k) * Z * p.NW +
                                                                         (int64_t)z * p.NW + cb0 + 4 * pc));
 #pragma unroll
@@ -77,16 +84,14 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) sraw[r] = srow[(int64_t)r * p.NW];
 
+  int beta[8];  // midpoint bias of each row's zone set (0: every zone active)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U) + 128
+    beta[e] = DENSE ? 0 : midpoint_bias<Z>(zone_bits<Z>(p.sigma[k0 + e], p.thr.t));
+    D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U & mask) + 128
 #pragma unroll
     for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
   }
-  // every zone active: beta = 0, u - c_row = w * 2^SH
-  const uint16_t nc = f32_to_f16_bits(-(float)(1024 + (128 >> SH)));
-  const uint32_t negc = (uint32_t)nc | ((uint32_t)nc << 16);
-  const float cb = 128.f;
 
   uint16_t* dst = p.wt + (int64_t)c * p.K + k0;
 #pragma unroll
@@ -94,6 +99,11 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
     uint32_t out[4][4];  // [beta][pair]
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
+      // u - c_row = w_eff * 2^SH for the pair's two rows
+      const uint16_t c0 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[2 * pp]));
+      const uint16_t c1 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[2 * pp + 1]));
+      const uint32_t negc = (uint32_t)c0 | ((uint32_t)c1 << 16);
+      const float cb0 = (float)(128 - beta[2 * pp] * (1 << SH)), cb1 = (float)(128 - beta[2 * pp + 1] * (1 << SH));
       uint32_t V[2];
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
@@ -111,7 +121,7 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
           out[b][pp] = Dequant<F16, SH>::pair(V[0], V[1], b, negc, (uint32_t)s | ((uint32_t)s << 16));
         } else {
           const float sf = to_f32<DT>(s) * (1.0f / (float)(1 << SH));
-          out[b][pp] = Dequant<BF16, SH>::pair_bf16(V[0], V[1], b, cb, cb, sf);
+          out[b][pp] = Dequant<BF16, SH>::pair_bf16(V[0], V[1], b, cb0, cb1, sf);
         }
       }
     }
@@ -123,15 +133,38 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   }
 }
 
+// Graded products: a row of x holding a non-finite value has every output
+// non-finite, and the graded kernels return those outputs as NaN (see
+// graded_nonfinite_to_nan); the library GEMM leaves inf where the fused
+// kernels give NaN, so this pass (one block per row, after the GEMM) scans
+// the row's activations and writes NaN over its outputs if one is not finite.
 template <typename DT>
+__global__ __launch_bounds__(256) void nonfinite_rows_to_nan_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                    int K, uint16_t* __restrict__ y, int N) {
+  constexpr uint32_t EXP = DT::id == F16::id ? 0x7C00u : 0x7F80u;  // all-ones exponent: inf or NaN
+  const int m = blockIdx.x;
+  const uint16_t* xr = x + (int64_t)m * ldx;
+  int bad = 0;
+  for (int i = threadIdx.x; i < K / 8; i += 256) {  // ldx % 8 == 0, x 16-byte aligned
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + 8 * i);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      bad |= ((v[q] & EXP) == EXP) | (((v[q] >> 16) & EXP) == EXP);
+  }
+  if (!__syncthreads_or(bad)) return;
+  const uint16_t nan = DT::id == F16::id ? 0x7E00u : 0x7FC0u;
+  for (int n = threadIdx.x; n < N; n += 256) y[(int64_t)m * N + n] = nan;
+}
+
+template <typename DT, bool DENSE>
 int launch_dequant_dt(const DequantParams& p, int max_bits, hipStream_t st) {
   const dim3 grid((unsigned)((p.NW + kDqColsPerBlock - 1) / kDqColsPerBlock),
                   (unsigned)((p.K + kDqRowsPerBlock - 1) / kDqRowsPerBlock));
   switch (max_bits) {
-    case 2: launch_main_kernel(dequant_nk_kernel<DT, 1>, grid, dim3(256), st, p); break;
-    case 4: launch_main_kernel(dequant_nk_kernel<DT, 2>, grid, dim3(256), st, p); break;
-    case 6: launch_main_kernel(dequant_nk_kernel<DT, 3>, grid, dim3(256), st, p); break;
-    case 8: launch_main_kernel(dequant_nk_kernel<DT, 4>, grid, dim3(256), st, p); break;
+    case 2: launch_main_kernel(dequant_nk_kernel<DT, 1, DENSE>, grid, dim3(256), st, p); break;
+    case 4: launch_main_kernel(dequant_nk_kernel<DT, 2, DENSE>, grid, dim3(256), st, p); break;
+    case 6: launch_main_kernel(dequant_nk_kernel<DT, 3, DENSE>, grid, dim3(256), st, p); break;
+    case 8: launch_main_kernel(dequant_nk_kernel<DT, 4, DENSE>, grid, dim3(256), st, p); break;
     default: return GRINQH_ERR_INVALID;
   }
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
@@ -140,11 +173,23 @@ int launch_dequant_dt(const DequantParams& p, int max_bits, hipStream_t st) {
 }  // namespace
 
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
-                      int max_bits, int dtype, hipStream_t st) {
+                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st) {
   if (K % 32 != 0 || N % 64 != 0 || gs % 32 != 0 || (int64_t)K * N >= ((int64_t)1 << 40)) return GRINQH_ERR_INVALID;
-  DequantParams p{planes, scale, wt, K, N, N / 16, gs};
-  return dtype == GRINQH_DTYPE_BF16 ? launch_dequant_dt<BF16>(p, max_bits, st)
-                                    : launch_dequant_dt<F16>(p, max_bits, st);
+  const DequantParams p{planes, scale, wt, sigma, thr, K, N, N / 16, gs};
+  const bool bf16 = dtype == GRINQH_DTYPE_BF16;
+  if (sigma == nullptr)
+    return bf16 ? launch_dequant_dt<BF16, true>(p, max_bits, st) : launch_dequant_dt<F16, true>(p, max_bits, st);
+  return bf16 ? launch_dequant_dt<BF16, false>(p, max_bits, st) : launch_dequant_dt<F16, false>(p, max_bits, st);
+}
+
+int launch_nonfinite_rows_to_nan(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* y, int N, int dtype,
+                                 hipStream_t st) {
+  if (M <= 0) return GRINQH_OK;
+  if (dtype == GRINQH_DTYPE_BF16)
+    hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel<BF16>, dim3(M), dim3(256), 0, st, x, ldx, K, y, N);
+  else
+    hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel<F16>, dim3(M), dim3(256), 0, st, x, ldx, K, y, N);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 
 }  // namespace grinqh

@@ -108,16 +108,20 @@ int prefill_block_rows(int64_t M, int64_t N);
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
 
-// Dense prefill from kLibraryGemmRows rows (and N % 64 == 0): the dense
-// weight Wt[N][K] = RNE(w * s) is written once (dequant.hip), then a library
-// GEMM multiplies it (blas.hip); below, and for other N, the fused
-// dequantize-into-LDS kernel.  Graded batches always take the fused kernel.
-// (At 256 rows the fused kernel was faster for all four Llama-3-8B shapes, at
-// 512 slower for three of them, at 2048 rows 1.5-1.9x slower.)
+// Prefill from kLibraryGemmRows rows (and N % 64 == 0): the weight Wt[N][K] =
+// RNE(w * s) (graded: RNE(w_eff * s) from the union statistic) is written
+// once (dequant.hip), then a library GEMM multiplies it (blas.hip); below,
+// and for other N, the fused dequantize-into-LDS kernel.  (Dense: at 256 rows
+// the fused kernel was faster for all four Llama-3-8B shapes, at 512 slower
+// for three of them, at 2048 rows 1.5-1.9x slower.)
 constexpr int64_t kLibraryGemmRows = 512;
 constexpr size_t kLibraryGemmWorkspace = size_t(32) << 20;
+// sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
-                      int max_bits, int dtype, hipStream_t st);
+                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st);
+// graded library path: rows of x holding a non-finite value get NaN outputs
+int launch_nonfinite_rows_to_nan(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* y, int N, int dtype,
+                                 hipStream_t st);
 // y[M][N] = x[M][K] @ wt[N][K]^T (+ bias) in the activation dtype, fp32 accumulation
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
               int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes, hipStream_t st);
