@@ -49,6 +49,7 @@ void arm_kernel_timing() {
 struct WorkspaceLayout {
   size_t counter_off, sigma_off, perm_off, stage_off, xsort_off, partial_off, total;
   size_t wt_off, blas_off;  // library-GEMM prefill: dense weight [N][K], then the GEMM's workspace
+  size_t chunk_off, flag_off;  // graded library-GEMM prefill: statistic partials, non-finite row flags
   bool library_gemm;
   DecodePlan plan;
 };
@@ -71,10 +72,15 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 // workspace shared by calls of different shapes keeps them zero.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
-  if (M >= kLibraryGemmRows && N % 64 == 0) {  // [counters | sigma (graded) | Wt | GEMM workspace]
+  // [counters | graded: sigma, its chunk maxima, row flags | Wt | GEMM workspace]
+  if (M >= kLibraryGemmRows && N % 64 == 0) {
+    const bool g = mode == GRINQH_MODE_UNION;
+    const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.library_gemm = true;
     w.sigma_off = kCounterBytes;
-    w.wt_off = w.sigma_off + (mode == GRINQH_MODE_UNION ? round_up((size_t)K * sizeof(float), 256) : 0);
+    w.chunk_off = w.sigma_off + (g ? round_up((size_t)K * sizeof(float), 256) : 0);
+    w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
+    w.wt_off = w.flag_off + (g ? round_up((size_t)((K + 255) / 256) * (size_t)M, 256) : 0);
     w.blas_off = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
     w.total = w.blas_off + kLibraryGemmWorkspace;
     return w;
@@ -120,14 +126,17 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   if (wl.library_gemm) {  // the (graded) weight once, then the library GEMM
     uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
     float* sigma = graded ? reinterpret_cast<float*>(ws + wl.sigma_off) : nullptr;
-    int rc = graded ? launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st) : GRINQH_OK;
+    uint8_t* flags = reinterpret_cast<uint8_t*>(ws + wl.flag_off);
+    int rc = graded ? launch_sigma_chunks(xs, d.ldx, (int)M, d.K, dtype, reinterpret_cast<float*>(ws + wl.chunk_off),
+                                          flags, sigma, st)
+                    : GRINQH_OK;
     if (rc != GRINQH_OK) return rc;
     arm_kernel_timing();
     rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, st);
     t_kernel_timing = KernelTiming{};
     if (rc == GRINQH_OK)
       rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
-    if (rc == GRINQH_OK && graded) rc = launch_nonfinite_rows_to_nan(xs, d.ldx, (int)M, d.K, ys, d.N, dtype, st);
+    if (rc == GRINQH_OK && graded) rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);
     return rc;
   }
   PrefillParams p{};

@@ -133,26 +133,98 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   }
 }
 
+// Union statistic of a large graded batch, first pass: a block takes 256
+// columns (8 per lane, 16-byte loads) of a chunk of rows, 8 rows at a time,
+// and writes its column maxima to partial[chunk][k] (NaN ignored unless every
+// value is NaN, as fmaxf does).  It also records, per row, whether the row's
+// 256 values hold an inf or NaN: flags[column block][m].
+template <typename DT>
+__global__ __launch_bounds__(256) void sigma_chunks_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
+                                                           int rows_per_chunk, float* __restrict__ partial,
+                                                           uint8_t* __restrict__ flags) {
+  constexpr uint32_t EXP = DT::id == F16::id ? 0x7C00u : 0x7F80u;  // all-ones exponent: inf or NaN
+  __shared__ float s_part[8][256 + 4];
+  const int l = threadIdx.x & 31, g = threadIdx.x >> 5;
+  const int k = blockIdx.x * 256 + 8 * l;
+  const bool col_ok = k < K;  // K % 8 == 0: a lane's 8 columns are all in or all out
+  const int r0 = blockIdx.y * rows_per_chunk, r1 = min(r0 + rows_per_chunk, M);
+  float s[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s[i] = __int_as_float(0x7fc00000);  // NaN: no row seen yet
+  for (int mb = r0 + g; mb < r1; mb += 32) {  // 4 rows' loads in flight
+    u32x4_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = mb + 8 * j;
+      v[j] = u32x4_t{0u, 0u, 0u, 0u};
+      if (col_ok && m < r1) v[j] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)m * ldx + k);  // ldx % 8 == 0
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = mb + 8 * j;
+      if (m >= r1) break;  // the same for the 32 lanes of a row
+      bool bad = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint16_t lo = (uint16_t)(v[j][q] & 0xFFFFu), hi = (uint16_t)(v[j][q] >> 16);
+        s[2 * q] = fmaxf(s[2 * q], fabsf(to_f32<DT>(lo)));
+        s[2 * q + 1] = fmaxf(s[2 * q + 1], fabsf(to_f32<DT>(hi)));
+        bad |= ((lo & EXP) == EXP) | ((hi & EXP) == EXP);
+      }
+      // the 32 lanes of this half-wave share row m (lanes of a finished half read as 0)
+      const uint64_t bal = __ballot(bad);
+      if (l == 0) flags[(int64_t)blockIdx.x * M + m] = ((bal >> (threadIdx.x & 32)) & 0xFFFFFFFFull) != 0;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s_part[g][8 * l + i] = s[i];
+  __syncthreads();
+  const int kk = blockIdx.x * 256 + threadIdx.x;
+  if (kk < K) {
+    float r = s_part[0][threadIdx.x];
+#pragma unroll
+    for (int gg = 1; gg < 8; ++gg) r = fmaxf(r, s_part[gg][threadIdx.x]);
+    partial[(int64_t)blockIdx.y * K + kk] = r;
+  }
+}
+
+// Second pass: sigma[k] = fmaxf over the chunks' maxima (exact in any order).
+// A block takes 64 columns; its 4 waves take every 4th chunk, 4 loads in
+// flight each, and combine through LDS.
+__global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* __restrict__ partial, int chunks,
+                                                                  int K, float* __restrict__ sigma) {
+  __shared__ float s_part[4][64];
+  const int cl = threadIdx.x & 63, cg = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + cl;
+  const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
+  float s = __int_as_float(0x7fc00000);
+  for (int c0 = cg; c0 < chunks; c0 += 16) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = min(c0 + 4 * j, chunks - 1);  // past the end: repeats the last chunk
+      v[j] = partial[(int64_t)c * K + kc];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s = fmaxf(s, v[j]);
+  }
+  s_part[cg][cl] = s;
+  __syncthreads();
+  if (cg == 0 && k < K) sigma[k] = fmaxf(fmaxf(s_part[0][cl], s_part[1][cl]), fmaxf(s_part[2][cl], s_part[3][cl]));
+}
+
 // Graded products: a row of x holding a non-finite value has every output
 // non-finite, and the graded kernels return those outputs as NaN (see
 // graded_nonfinite_to_nan); the library GEMM leaves inf where the fused
-// kernels give NaN, so this pass (one block per row, after the GEMM) scans
-// the row's activations and writes NaN over its outputs if one is not finite.
-template <typename DT>
-__global__ __launch_bounds__(256) void nonfinite_rows_to_nan_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                    int K, uint16_t* __restrict__ y, int N) {
-  constexpr uint32_t EXP = DT::id == F16::id ? 0x7C00u : 0x7F80u;  // all-ones exponent: inf or NaN
+// kernels give NaN, so this pass (one block per row, after the GEMM) writes
+// NaN over the outputs of every row that the statistic pass flagged.
+__global__ __launch_bounds__(256) void nonfinite_rows_to_nan_kernel(const uint8_t* __restrict__ flags, int col_blocks,
+                                                                    int M, uint16_t* __restrict__ y, int N,
+                                                                    uint16_t nan) {
   const int m = blockIdx.x;
-  const uint16_t* xr = x + (int64_t)m * ldx;
   int bad = 0;
-  for (int i = threadIdx.x; i < K / 8; i += 256) {  // ldx % 8 == 0, x 16-byte aligned
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + 8 * i);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      bad |= ((v[q] & EXP) == EXP) | (((v[q] >> 16) & EXP) == EXP);
-  }
+  for (int i = threadIdx.x; i < col_blocks; i += 256) bad |= flags[(int64_t)i * M + m];
   if (!__syncthreads_or(bad)) return;
-  const uint16_t nan = DT::id == F16::id ? 0x7E00u : 0x7FC0u;
   for (int n = threadIdx.x; n < N; n += 256) y[(int64_t)m * N + n] = nan;
 }
 
@@ -182,13 +254,25 @@ int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* w
   return bf16 ? launch_dequant_dt<BF16, false>(p, max_bits, st) : launch_dequant_dt<F16, false>(p, max_bits, st);
 }
 
-int launch_nonfinite_rows_to_nan(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* y, int N, int dtype,
-                                 hipStream_t st) {
-  if (M <= 0) return GRINQH_OK;
+int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
+                        float* sigma, hipStream_t st) {
+  if (M <= 0 || K <= 0 || K % 8 != 0) return GRINQH_ERR_INVALID;
+  const int rows = sigma_chunk_rows(M), chunks = (M + rows - 1) / rows;
+  const dim3 grid((unsigned)((K + 255) / 256), (unsigned)chunks);
   if (dtype == GRINQH_DTYPE_BF16)
-    hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel<BF16>, dim3(M), dim3(256), 0, st, x, ldx, K, y, N);
+    hipLaunchKernelGGL(sigma_chunks_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
   else
-    hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel<F16>, dim3(M), dim3(256), 0, st, x, ldx, K, y, N);
+    hipLaunchKernelGGL(sigma_chunks_kernel<F16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
+  hipLaunchKernelGGL(sigma_chunks_reduce_kernel, dim3((unsigned)((K + 63) / 64)), dim3(256), 0, st, partial, chunks, K,
+                     sigma);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
+}
+
+int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st) {
+  if (M <= 0) return GRINQH_OK;
+  const uint16_t nan = dtype == GRINQH_DTYPE_BF16 ? 0x7FC0u : 0x7E00u;
+  hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel, dim3((unsigned)M), dim3(256), 0, st, flags, (K + 255) / 256, M, y,
+                     N, nan);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

@@ -119,9 +119,18 @@ constexpr size_t kLibraryGemmWorkspace = size_t(32) << 20;
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
                       int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st);
-// graded library path: rows of x holding a non-finite value get NaN outputs
-int launch_nonfinite_rows_to_nan(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* y, int N, int dtype,
-                                 hipStream_t st);
+// Union statistic of a graded library-path batch in two passes: column
+// maxima of row chunks (partial: chunks x K floats), then their maximum
+// (sigma: K floats); flags (ceil(K/256) x M bytes) marks the rows holding an
+// inf or NaN.  Chunks of at least 32 rows, at most 64 chunks.
+inline int sigma_chunk_rows(int64_t M) {
+  const int64_t r = ((M + 63) / 64 + 7) / 8 * 8;
+  return (int)(r > 32 ? r : 32);
+}
+int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
+                        float* sigma, hipStream_t st);
+// after the GEMM: the outputs of every flagged row become NaN
+int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st);
 // y[M][N] = x[M][K] @ wt[N][K]^T (+ bias) in the activation dtype, fp32 accumulation
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
               int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes, hipStream_t st);
