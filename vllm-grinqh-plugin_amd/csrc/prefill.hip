@@ -401,12 +401,22 @@ int prefill_block_rows(int64_t M, int64_t N) {
 int prefill_splits(int64_t M, int64_t K, int64_t N) {
   const int64_t BM = prefill_block_rows(M, N);
   const int64_t blocks = ((N / 16 + 15) / 16) * ((M + BM - 1) / BM);
-  int64_t splits = (kTargetBlocks + blocks - 1) / blocks;
+  int64_t cap = (kTargetBlocks + blocks - 1) / blocks;  // enough ranges for a block per CU
   const int64_t by_k = K / 256;
-  if (splits > by_k) splits = by_k;
+  if (cap > by_k) cap = by_k;
   const int64_t by_bytes = (int64_t)kMaxPrefillPartialBytes / (M * N * 4);
-  if (splits > by_bytes) splits = by_bytes;
-  return splits > 1 ? (int)splits : 1;
+  if (cap > by_bytes) cap = by_bytes;
+  // One block per CU: a launch takes ceil(blocks * s / 256) rounds of K / s
+  // rows each.  Take the s <= cap with the fewest rounds per range (the
+  // fewest ranges on a tie): 24 column blocks split 11 ways would start a
+  // second round for 8 blocks, split 10 ways they fit one.
+  int64_t best = 1;
+  for (int64_t s = 2; s <= cap; ++s) {
+    const int64_t rounds = (blocks * s + kTargetBlocks - 1) / kTargetBlocks;
+    const int64_t best_rounds = (blocks * best + kTargetBlocks - 1) / kTargetBlocks;
+    if (rounds * best < best_rounds * s) best = s;
+  }
+  return (int)best;
 }
 
 // Stage rows and stages in flight per configuration.  256-row tiles (fp16,
