@@ -339,14 +339,15 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
 @pytest.mark.parametrize("max_bits", [4, 8])
 @pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0], None],
                          ids=["non_monotone", "skip_all", "all_planes", "tied", "quantiles"])
-def test_prefill_library_gemm_graded(t, max_bits, dtype):
-    """Graded (union) batches of 512 rows and more: the dequant kernel writes
+@pytest.mark.parametrize("M", [300, 512])
+def test_prefill_library_gemm_graded(M, t, max_bits, dtype):
+    """Graded (union) batches of 256 rows and more: the dequant kernel writes
     RNE(w_eff * s) from each row's zone set (inactive planes not fetched,
     midpoint bias added), then the library GEMM.  Zone sets that are not
     prefixes, none, all, tied thresholds and the 70/20/8/2 % quantile mix, held
     to S10 within the weight-rounding bound, with bias."""
     from grinqh.kernel import run_product
-    M, K, N = 512, 1056, 512  # K % 64 == 32: the last dequant tile is half full
+    K, N = 1056, 512  # K % 64 == 32: the last dequant tile is half full
     rng = np.random.default_rng(4321 + max_bits)
     W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)
     if t is None:

@@ -108,13 +108,16 @@ int prefill_block_rows(int64_t M, int64_t N);
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
 
-// Prefill from kLibraryGemmRows rows (and N % 64 == 0): the weight Wt[N][K] =
-// RNE(w * s) (graded: RNE(w_eff * s) from the union statistic) is written
-// once (dequant.hip), then a library GEMM multiplies it (blas.hip); below,
-// and for other N, the fused dequantize-into-LDS kernel.  (Dense: at 256 rows
-// the fused kernel was faster for all four Llama-3-8B shapes, at 512 slower
-// for three of them, at 2048 rows 1.5-1.9x slower.)
+// Prefill from kLibraryGemmRows rows, graded from kLibraryGemmRowsGraded (and
+// N % 64 == 0): the weight Wt[N][K] = RNE(w * s) (graded: RNE(w_eff * s)
+// from the union statistic) is written once (dequant.hip), then a library
+// GEMM multiplies it (blas.hip); below, and for other N, the fused
+// dequantize-into-LDS kernel.  (Dense: at 256 rows the fused kernel was
+// faster for all four Llama-3-8B shapes, at 512 slower for three of them, at
+// 2048 rows 1.5-1.9x slower.  Graded: at 192 rows the fused kernel took 361 us
+// for the four shapes against 390, at 256 rows 392 against 379.)
 constexpr int64_t kLibraryGemmRows = 512;
+constexpr int64_t kLibraryGemmRowsGraded = 256;
 constexpr size_t kLibraryGemmWorkspace = size_t(32) << 20;
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
