@@ -393,6 +393,25 @@ def test_graph_capture_library_prefill(mode):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("mode", ["dense", "union"])
+def test_prefill_library_gemm_70b_qkv_shape(mode):
+    """Llama-3-70B qkv (K=8192, N=10240) at 4096 rows, every plane active: the
+    shape whose first hipBLASLt heuristic choice asked for more GEMM workspace
+    than it was allowed.  The first 64 output rows are held to the oracle (S9;
+    with every zone active the graded weight is the dense one)."""
+    from grinqh.kernel import run_product
+    M, K, N, b, R = 4096, 8192, 10240, 8, 64
+    rng = np.random.default_rng(70)
+    W = rand_weight(rng, K, N, b)
+    s = to_dtype_np(rng.standard_normal((K // 128, N)) * 0.05, "float16")
+    x = to_dtype_np(rng.standard_normal((M, K)), "float16")
+    y = run_product(_tdt(x, "float16"), _prepare(W, b), _tdt(s, "float16"), None, b, 128, N // 4, [-1.0] * 4, mode)
+    xs = x[:R]
+    assert_output_close(y[:R], O.dense_prefill_f64(xs, W, s, 128, "float16"),
+                        O.dense_prefill(xs, W, s, None, 128, "float16"), "float16",
+                        what=f"70B qkv M={M} {mode}", extra_tol=dense_rounding_bound(xs, W, s, "float16"))
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_library_gemm_strided_rows(dtype):
     """Library-GEMM prefill of activation rows with a leading dimension above

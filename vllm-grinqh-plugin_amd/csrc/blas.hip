@@ -5,7 +5,7 @@
 // and its bias add (:707-708).  The weight comes from dequant.hip, stored
 // K-contiguous: in hipBLASLt's column-major terms D (N x M, ld N) =
 // op(A) * B with A = Wt (K x N, ld K, transposed) and B = X (K x M, ld ldx),
-// the "TN" form, which ran 10-40 % faster here than the K x N weight.
+// the "TN" form, which ran 10-55 % faster here than the K x N weight.
 //
 // The bias goes through the GEMM's bias epilogue: y = RNE(acc + bias), one
 // rounding, where the reference rounds twice (RNE(RNE(acc) + bias)); the two
@@ -17,6 +17,7 @@
 // enqueues the GEMM.
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
 #include <mutex>
 #include <vector>
 
@@ -60,12 +61,24 @@ struct GemmPlan {
   size_t algo_ws;
 };
 
-// Builds the descriptors of one shape and asks the heuristic for its best
-// algorithm within ws_bytes of workspace.
+// A failure of the library is reported on stderr with its status (the C ABI
+// returns GRINQH_ERR_HIP): which step failed is otherwise not visible.
+bool blas_failed(const char* what, int status, const GemmShape& s) {
+  std::fprintf(stderr, "grinqh: hipBLASLt %s failed (status %d) for M=%lld N=%lld K=%lld ldx=%lld dtype=%d\n", what,
+               status, (long long)s.M, (long long)s.N, (long long)s.K, (long long)s.ldx, s.dtype);
+  return false;
+}
+
+// Builds the descriptors of one shape and takes the heuristic's best
+// algorithm whose workspace fits ws_bytes.  The heuristic does not always
+// honour the workspace limit of the preference (Llama-3-70B qkv at 4096 rows:
+// its first choice asked for 57 MiB of 32), so several candidates are
+// requested and the first that fits is kept.
 bool make_plan(const GemmShape& s, GemmPlan& pl) {
   const hipDataType dt = s.dtype == GRINQH_DTYPE_BF16 ? HIP_R_16BF : HIP_R_16F;
   pl.shape = s;
-  if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return false;
+  if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+    return blas_failed("matmul descriptor", -1, s);
   const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
   hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT));
   hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN));
@@ -78,20 +91,27 @@ bool make_plan(const GemmShape& s, GemmPlan& pl) {
   if (hipblasLtMatrixLayoutCreate(&pl.a, dt, (uint64_t)s.K, (uint64_t)s.N, s.K) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&pl.b, dt, (uint64_t)s.K, (uint64_t)s.M, s.ldx) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&pl.d, dt, (uint64_t)s.N, (uint64_t)s.M, s.N) != HIPBLAS_STATUS_SUCCESS)
-    return false;
+    return blas_failed("matrix layout", -1, s);
   hipblasLtMatmulPreference_t pref = nullptr;
-  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return blas_failed("preference", -1, s);
   const uint64_t ws = s.ws_bytes;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-  hipblasLtMatmulHeuristicResult_t res[1];
+  constexpr int kCandidates = 16;
+  hipblasLtMatmulHeuristicResult_t res[kCandidates];
   int found = 0;
   const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle_for_device(s.dev), pl.desc, pl.a, pl.b, pl.d,
-                                                             pl.d, pref, 1, res, &found);
+                                                             pl.d, pref, kCandidates, res, &found);
   hipblasLtMatmulPreferenceDestroy(pref);
-  if (st != HIPBLAS_STATUS_SUCCESS || found < 1 || res[0].workspaceSize > s.ws_bytes) return false;
-  pl.algo = res[0].algo;
-  pl.algo_ws = res[0].workspaceSize;
-  return true;
+  if (st != HIPBLAS_STATUS_SUCCESS || found < 1)
+    return blas_failed("heuristic", st == HIPBLAS_STATUS_SUCCESS ? -2 : (int)st, s);
+  for (int i = 0; i < found && i < kCandidates; ++i) {
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= s.ws_bytes) {
+      pl.algo = res[i].algo;
+      pl.algo_ws = res[i].workspaceSize;
+      return true;
+    }
+  }
+  return blas_failed("heuristic (no candidate within the workspace)", -3, s);
 }
 
 }  // namespace
@@ -120,7 +140,11 @@ int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t
   const float alpha = 1.f, beta = 0.f;
   const hipblasStatus_t s = hipblasLtMatmul(h, pl->desc, &alpha, wt, pl->a, x, pl->b, &beta, y, pl->d, y, pl->d,
                                             &pl->algo, ws, pl->algo_ws, st);
-  return s == HIPBLAS_STATUS_SUCCESS ? GRINQH_OK : GRINQH_ERR_HIP;
+  if (s != HIPBLAS_STATUS_SUCCESS) {
+    blas_failed("matmul", s, key);
+    return GRINQH_ERR_HIP;
+  }
+  return GRINQH_OK;
 }
 
 }  // namespace grinqh

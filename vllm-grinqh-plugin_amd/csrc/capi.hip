@@ -124,6 +124,9 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
   if (wl.library_gemm) {  // the (graded) weight once, then the library GEMM
+    // an error a library left in this thread's last-error slot must not be
+    // taken for a failure of the launches below
+    (void)hipGetLastError();
     uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
     float* sigma = graded ? reinterpret_cast<float*>(ws + wl.sigma_off) : nullptr;
     uint8_t* flags = reinterpret_cast<uint8_t*>(ws + wl.flag_off);
@@ -136,7 +139,10 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     t_kernel_timing = KernelTiming{};
     if (rc == GRINQH_OK)
       rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
-    if (rc == GRINQH_OK && graded) rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);
+    if (rc == GRINQH_OK && graded) {
+      (void)hipGetLastError();  // the GEMM's library calls may leave one behind as well
+      rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);
+    }
     return rc;
   }
   PrefillParams p{};

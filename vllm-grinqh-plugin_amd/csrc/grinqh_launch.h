@@ -118,7 +118,7 @@ int prefill_splits(int64_t M, int64_t K, int64_t N);
 // for the four shapes against 390, at 256 rows 392 against 379.)
 constexpr int64_t kLibraryGemmRows = 512;
 constexpr int64_t kLibraryGemmRowsGraded = 256;
-constexpr size_t kLibraryGemmWorkspace = size_t(32) << 20;
+constexpr size_t kLibraryGemmWorkspace = size_t(128) << 20;  // hipBLASLt's stream-K algorithms ask up to ~60 MiB
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
                       int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st);
