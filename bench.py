@@ -78,6 +78,31 @@ def thresholds_for(x, q=(0.5, 0.8, 0.95)):
     return [0.0] + [float(v) for v in np.quantile(sigma, q)]
 
 
+def graph_time_us(torch, stream, call, n_it: int, replays: int = 3) -> float:
+    """Per-call GPU time of call(0) .. call(n_it - 1) captured in one HIP graph
+    and replayed `replays` times between two events, so the host's launch cost
+    (Python, ctypes, the GEMM library's host side) is not counted: the time of
+    the products themselves.  Two eager calls first size the workspace and
+    plan the library GEMM."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for j in range(2):
+            call(j)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for j in range(n_it):
+                call(j)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(replays):
+            g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (replays * n_it)
+
+
 def decode_bytes(bits_per_row, K, N, M):
     planes = int(bits_per_row.sum()) * (N // 4)
     return planes + (K // GS) * N * 2 + M * K * 2 + M * N * 2
@@ -310,18 +335,9 @@ def main() -> int:
         prefill = []
         for i, (name, K, N) in enumerate(SHAPES):
             x = synth_x(torch, PREFILL_M, K, 99 + i, dev)
-            p, s = copies[name][0]
-            with torch.cuda.stream(stream):
-                run_product(x, p, s, None, BITS, GS, N // 4, [0.0] * 4, "dense")
-                torch.cuda.synchronize()
-                e0.record(stream)
-                n_it = 5
-                for j in range(n_it):
-                    pj, sj = copies[name][j % n_copies]
-                    run_product(x, pj, sj, None, BITS, GS, N // 4, [0.0] * 4, "dense")
-                e1.record(stream)
-            e1.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / n_it
+            cps = copies[name]
+            us = graph_time_us(torch, stream, lambda j: run_product(
+                x, cps[j % n_copies][0], cps[j % n_copies][1], None, BITS, GS, N // 4, [0.0] * 4, "dense"), 5)
             tf = 2.0 * PREFILL_M * K * N / (us * 1e-6) / 1e12
             prefill.append({"shape": name, "M": PREFILL_M, "us": round(us, 2), "tflops": round(tf, 1),
                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
@@ -336,18 +352,9 @@ def main() -> int:
             for M in PREFILL_GRADED_M:
                 x = synth_x(torch, M, K, 199 + i, dev)
                 t = thresholds_for(x, (0.7, 0.9, 0.98))
-                p, s = copies[name][0]
-                with torch.cuda.stream(stream):
-                    run_product(x, p, s, None, BITS, GS, N // 4, t, "union")
-                    torch.cuda.synchronize()
-                    e0.record(stream)
-                    n_it = 3
-                    for j in range(n_it):
-                        pj, sj = copies[name][j % n_copies]
-                        run_product(x, pj, sj, None, BITS, GS, N // 4, t, "union")
-                    e1.record(stream)
-                e1.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / n_it
+                cps = copies[name]
+                us = graph_time_us(torch, stream, lambda j: run_product(
+                    x, cps[j % n_copies][0], cps[j % n_copies][1], None, BITS, GS, N // 4, t, "union"), 3)
                 tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
                 prefill_graded.append({"shape": name, "M": M, "us": round(us, 2), "tflops": round(tf, 1),
                                        "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})

@@ -362,13 +362,15 @@ def test_prefill_library_gemm_graded(M, t, max_bits, dtype):
                         extra_tol=graded_rounding_bound(x, W, s, t, max_bits, dtype))
 
 
-@pytest.mark.parametrize("mode", ["dense", "union"])
-def test_graph_capture_library_prefill(mode):
-    """A 512-row product (dequant kernel, library GEMM, graded row pass)
+@pytest.mark.parametrize("mode,M,K,N", [("dense", 512, 2048, 1024), ("union", 512, 2048, 1024),
+                                        ("dense", 2048, 4096, 28672), ("union", 2048, 4096, 28672)],
+                         ids=["dense-512", "union-512", "dense-gate_up-2048", "union-gate_up-2048"])
+def test_graph_capture_library_prefill(mode, M, K, N):
+    """A library-path product (dequant kernel, library GEMM, graded row pass)
     captured in a HIP graph and replayed several times with eager work in
-    between matches the eager result on every replay."""
+    between matches the eager result on every replay.  The gate_up shape at
+    2048 rows takes the library's stream-K GEMM, which uses its workspace."""
     from grinqh.kernel import run_product
-    M, K, N = 512, 2048, 1024
     rng = np.random.default_rng(88)
     W, x, s = _setup(rng, K, N, 8, "float16", M=M, scale_sd=0.01)
     P, st = _prepare(W, 8), _tdt(s, "float16")
@@ -388,7 +390,7 @@ def test_graph_capture_library_prefill(mode):
         yg.zero_()
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(yg, eager), f"replay {i}"
+        assert torch.equal(yg, eager), f"replay {i}: max |diff| {(yg.float() - eager.float()).abs().max().item()}"
         _ = run_product(xin, P, st, None, 8, 128, N // 4, t, mode)
         torch.cuda.synchronize()
 
