@@ -317,13 +317,16 @@ def test_prefill_256_row_tiles(dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("max_bits", BITS)
-@pytest.mark.parametrize("M,K,N", [(512, 96, 256), (700, 512, 768), (512, 2080, 320), (600, 256, 4112)])
+@pytest.mark.parametrize("M,K,N", [(512, 96, 256), (700, 512, 768), (512, 2080, 320), (600, 256, 4112),
+                                   (300, 256, 28672)])
 def test_prefill_library_gemm(M, K, N, max_bits, dtype):
-    """Dense batches of 512 rows and more: the dense weight Wt[N][K] is written
-    once (dequant kernel: 64-row tiles, the last one partial when K % 64 ==
-    32; scale groups of 128 crossing tiles), then the library GEMM multiplies
-    it with the bias in its epilogue.  N / 16 not a multiple of 4 (4112) keeps
-    the fused kernel.  Held to S9 like the fused kernel."""
+    """Dense batches of 512 rows and more, and of 257-511 rows when the fused
+    grid would need more than one round (300 x 28672): the dense weight
+    Wt[N][K] is written once (dequant kernel: 64-row tiles, the last one
+    partial when K % 64 == 32; scale groups of 128 crossing tiles), then the
+    library GEMM multiplies it with the bias in its epilogue.  N / 16 not a
+    multiple of 4 (4112) keeps the fused kernel.  Held to S9 like the fused
+    kernel."""
     from grinqh.kernel import run_product
     rng = np.random.default_rng(M * 7 + K + N + max_bits)
     W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)

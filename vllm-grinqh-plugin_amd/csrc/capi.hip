@@ -73,7 +73,7 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   // [counters | graded: sigma, its chunk maxima, row flags | Wt | GEMM workspace]
-  if (M >= (mode == GRINQH_MODE_UNION ? kLibraryGemmRowsGraded : kLibraryGemmRows) && N % 64 == 0) {
+  if (M > kDecodeMaxRows && use_library_gemm(M, N, mode == GRINQH_MODE_UNION)) {
     const bool g = mode == GRINQH_MODE_UNION;
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.library_gemm = true;

@@ -118,6 +118,17 @@ int prefill_splits(int64_t M, int64_t K, int64_t N);
 // for the four shapes against 390, at 256 rows 392 against 379.)
 constexpr int64_t kLibraryGemmRows = 512;
 constexpr int64_t kLibraryGemmRowsGraded = 256;
+// Whether a prefill product takes the library path.  Dense batches of
+// 257-511 rows take it too when the fused kernel's grid of 128-row tiles
+// needs more than one round of blocks (it is then not split over K, and each
+// round runs the whole K): gate_up at 320 rows took 213 us fused, 141 us here,
+// while qkv, o_proj and down (at most 96 blocks) stay within 15 us either way.
+inline bool use_library_gemm(int64_t M, int64_t N, bool graded) {
+  if (N % 64 != 0) return false;
+  if (graded) return M >= kLibraryGemmRowsGraded;
+  if (M >= kLibraryGemmRows) return true;
+  return M > 256 && ((N / 16 + 15) / 16) * ((M + 127) / 128) > kTargetBlocks;
+}
 constexpr size_t kLibraryGemmWorkspace = size_t(128) << 20;  // hipBLASLt's stream-K algorithms ask up to ~60 MiB
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
