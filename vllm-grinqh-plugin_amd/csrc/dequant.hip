@@ -6,8 +6,9 @@
 // fused prefill kernel.
 //
 // Replaces the dequantization half of grinqh_prefill_gemm_compiled
-// (grinqh/kernel.py:579-586: unpack_pyt + postshuffle + W * s, three torch
-// launches over int8 / fp16 copies of the weight).  The values are the same
+// (grinqh/kernel.py:571-586: unpack_pyt, sign extension, postshuffle, then
+// W * s, compiled torch passes over int8 and fp16 copies of the weight).  The
+// values are the same
 // RNE(w * s) the fused prefill kernel writes into LDS (Dequant<DT, SH>), so
 // both prefill paths multiply the same weight.
 //
