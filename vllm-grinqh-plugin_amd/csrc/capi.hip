@@ -119,7 +119,8 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
   return GRINQH_OK;
 }
 
-// M > kDecodeMaxRows: one prefill launch over the whole batch (graded batches
+// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm), else one fused
+// prefill launch over the whole batch (graded batches
 // first reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {

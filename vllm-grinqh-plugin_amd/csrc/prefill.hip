@@ -1,4 +1,5 @@
-// Prefill-regime GRINQH product (M > 64): dequantize-into-LDS GEMM on
+// Prefill-regime GRINQH product (M > 64, below the library-GEMM path of
+// dequant.hip / blas.hip): dequantize-into-LDS GEMM on
 // v_mfma_f32_16x16x32_{f16,bf16}, MFMA-bound.
 //
 // Replaces grinqh_prefill_gemm_compiled (grinqh/kernel.py:561-587: Wd =
