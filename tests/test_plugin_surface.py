@@ -157,6 +157,27 @@ def test_weight_loader_merged_shards(gq, bits):
         param.weight_loader(param, torch.zeros(64, 256, dtype=torch.int8), "x")
 
 
+def test_checkpoint_unpack_known_answers():
+    """Words derived by hand from compressed-tensors' published int32 packing
+    (field i of a word holds element i of its group at bits num_bits*i, values
+    stored offset by 2^(num_bits-1), trailing padding dropped), not from the
+    packer in grinqh/checkpoint.py: a big-endian field order or a two's
+    complement reading would fail them."""
+    from grinqh.checkpoint import unpack_from_int32
+    # 4 bits: values -8 -7 0 7 1 -1 3 -4 -> fields 0 1 8 15 9 7 11 4 -> 0x4B79F810
+    w4 = torch.tensor([[0x4B79F810]], dtype=torch.int32)
+    assert unpack_from_int32(w4, 4, (1, 8)).tolist() == [[-8, -7, 0, 7, 1, -1, 3, -4]]
+    # 8 bits: -128 127 0 -1 -> fields 0 255 128 127 -> 0x7F80FF00
+    w8 = torch.tensor([[0x7F80FF00]], dtype=torch.int32)
+    assert unpack_from_int32(w8, 8, (1, 4)).tolist() == [[-128, 127, 0, -1]]
+    # 2 bits: (-2 -1 0 1) x 4 -> fields 0 1 2 3 per byte -> 0xE4E4E4E4, a negative int32
+    w2 = torch.tensor([[0xE4E4E4E4 - (1 << 32)]], dtype=torch.int32)
+    assert unpack_from_int32(w2, 2, (1, 16)).tolist() == [[-2, -1, 0, 1] * 4]
+    # padding: 5 of 8 fields used (3 -5 0 7 -8 -> 0xF83B); the top 3 fields hold junk and are dropped
+    wp = torch.tensor([[0xF83B | (0x5A5 << 20)]], dtype=torch.int32)
+    assert unpack_from_int32(wp, 4, (1, 5)).tolist() == [[3, -5, 0, 7, -8]]
+
+
 def test_checkpoint_unpack_roundtrip():
     from grinqh.checkpoint import pack_to_int32, unpack_from_int32
     g = torch.Generator().manual_seed(3)
