@@ -80,13 +80,19 @@ bool make_plan(const GemmShape& s, GemmPlan& pl) {
   if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
     return blas_failed("matmul descriptor", -1, s);
   const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N;
-  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT));
-  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN));
+  if (hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) !=
+          HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) !=
+          HIPBLAS_STATUS_SUCCESS)
+    return blas_failed("transpose attributes", -1, s);
   if (s.bias) {
     const uint32_t epi = HIPBLASLT_EPILOGUE_BIAS;
     const int32_t bdt = dt;
-    hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi));
-    hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bdt, sizeof(bdt));
+    if (hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &epi, sizeof(epi)) !=
+            HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bdt, sizeof(bdt)) !=
+            HIPBLAS_STATUS_SUCCESS)
+      return blas_failed("bias epilogue attributes", -1, s);
   }
   if (hipblasLtMatrixLayoutCreate(&pl.a, dt, (uint64_t)s.K, (uint64_t)s.N, s.K) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&pl.b, dt, (uint64_t)s.K, (uint64_t)s.M, s.ldx) != HIPBLAS_STATUS_SUCCESS ||
@@ -95,7 +101,11 @@ bool make_plan(const GemmShape& s, GemmPlan& pl) {
   hipblasLtMatmulPreference_t pref = nullptr;
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return blas_failed("preference", -1, s);
   const uint64_t ws = s.ws_bytes;
-  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+  if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) !=
+      HIPBLAS_STATUS_SUCCESS) {
+    hipblasLtMatmulPreferenceDestroy(pref);
+    return blas_failed("workspace preference", -1, s);
+  }
   constexpr int kCandidates = 16;
   hipblasLtMatmulHeuristicResult_t res[kCandidates];
   int found = 0;
@@ -114,6 +124,15 @@ bool make_plan(const GemmShape& s, GemmPlan& pl) {
   return blas_failed("heuristic (no candidate within the workspace)", -3, s);
 }
 
+// Releases the descriptors of a plan that could not be completed.
+void destroy_plan(GemmPlan& pl) {
+  if (pl.a != nullptr) hipblasLtMatrixLayoutDestroy(pl.a);
+  if (pl.b != nullptr) hipblasLtMatrixLayoutDestroy(pl.b);
+  if (pl.d != nullptr) hipblasLtMatrixLayoutDestroy(pl.d);
+  if (pl.desc != nullptr) hipblasLtMatmulDescDestroy(pl.desc);
+  pl = GemmPlan{};
+}
+
 }  // namespace
 
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
@@ -129,13 +148,20 @@ int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t
     if (q.shape == key) pl = &q;
   if (pl == nullptr) {
     GemmPlan q{};
-    if (!make_plan(key, q)) return GRINQH_ERR_HIP;
+    if (!make_plan(key, q)) {
+      destroy_plan(q);
+      return GRINQH_ERR_HIP;
+    }
     plans.push_back(q);
     pl = &plans.back();
   }
   if (bias != nullptr) {
     const void* bp = bias;
-    hipblasLtMatmulDescSetAttribute(pl->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp));
+    if (hipblasLtMatmulDescSetAttribute(pl->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp)) !=
+        HIPBLAS_STATUS_SUCCESS) {
+      blas_failed("bias pointer", -1, key);
+      return GRINQH_ERR_HIP;
+    }
   }
   const float alpha = 1.f, beta = 0.f;
   const hipblasStatus_t s = hipblasLtMatmul(h, pl->desc, &alpha, wt, pl->a, x, pl->b, &beta, y, pl->d, y, pl->d,
