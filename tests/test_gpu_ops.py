@@ -345,7 +345,7 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
 @pytest.mark.parametrize("M", [300, 512])
 def test_prefill_library_gemm_graded(M, t, max_bits, dtype):
     """Graded (union) batches of 256 rows and more: the dequant kernel writes
-    RNE(w_eff * s) from each row's zone set (inactive planes not fetched,
+    RNE(w_eff * s) from each row's zone set (inactive planes masked to zero,
     midpoint bias added), then the library GEMM.  Zone sets that are not
     prefixes, none, all, tied thresholds and the 70/20/8/2 % quantile mix, held
     to S10 within the weight-rounding bound, with bias."""

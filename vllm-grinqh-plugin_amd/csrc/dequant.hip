@@ -2,8 +2,11 @@
 // activation dtype, stored K-contiguous ([N][K]), for the library GEMM that
 // follows (blas.hip).  Graded (union) batches write RNE(w_eff * s) instead,
 // with each row's zone set from sigma_k = max_m |x[m][k]|: the planes of its
-// inactive zones are not fetched and its midpoint bias is added, as in the
-// fused prefill kernel.
+// inactive zones are masked to zero and its midpoint bias is added, as in the
+// fused prefill kernel.  (Every plane is fetched: skipping the inactive ones
+// put a sigma load in front of each plane load, and with the 2-byte weight
+// write dominating the traffic that made the graded pass 15 % slower than
+// the dense one.)
 //
 // Replaces the dequantization half of grinqh_prefill_gemm_compiled
 // (grinqh/kernel.py:571-586: unpack_pyt, sign extension, postshuffle, then
@@ -56,9 +59,7 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
       const int seg = (threadIdx.x >> 3) + 32 * i;  // (k, z) of the block tile
       const int k = seg / Z, z = seg % Z;
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-      // graded: planes of inactive zones are not fetched (they read as zero)
-      const bool active = DENSE || (kb + k < p.K && ((zone_bits<Z>(p.sigma[kb + k], p.thr.t) >> z) & 1u));
-      if (kb + k < p.K && cb0 + 4 * pc < p.NW && active)
+      if (kb + k < p.K && cb0 + 4 * pc < p.NW)
         v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p.planes + (int64_t)(kb + k) * Z * p.NW +
                                                                         (int64_t)z * p.NW + cb0 + 4 * pc));
 #pragma unroll
@@ -88,7 +89,14 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   int beta[8];  // midpoint bias of each row's zone set (0: every zone active)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    beta[e] = DENSE ? 0 : midpoint_bias<Z>(zone_bits<Z>(p.sigma[k0 + e], p.thr.t));
+    if constexpr (!DENSE) {  // graded: inactive planes masked to zero
+      const uint32_t bits = zone_bits<Z>(p.sigma[k0 + e], p.thr.t);
+      beta[e] = midpoint_bias<Z>(bits);
+#pragma unroll
+      for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((bits >> z) & 1u);
+    } else {
+      beta[e] = 0;
+    }
     D[e][0] ^= 0xAAAAAAAAu;  // offset binary: u = int8(U & mask) + 128
 #pragma unroll
     for (int z = 1; z < Z; ++z) D[e][z] = rotr(D[e][z], (uint32_t)(2 * z));
