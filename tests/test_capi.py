@@ -60,16 +60,17 @@ def test_workspace_query(lib):
 def test_workspace_query_library_gemm_path(lib):
     """The large-batch prefill path (dequantized weight + library GEMM) sizes
     the workspace for the K-contiguous weight (2*N*K bytes) plus the GEMM's
-    128 MiB: dense from 512 rows, union from 256, dense 257-511 rows only when
-    the fused grid would need more than one round (gate_up's N), never when
-    N / 16 is not a multiple of 4."""
+    128 MiB: from 512 rows, at 257-511 rows only when the fused grid would
+    need more than one round (gate_up's N), never when N / 16 is not a
+    multiple of 4; dense and union alike."""
     K, gemm = 4096, 128 << 20
     dense, union = 2, 1
     library = lambda M, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode) >= 2 * N * K + gemm
     assert library(512, 6144, dense) and library(2048, 28672, dense)
     assert not library(511, 6144, dense) and not library(256, 28672, dense)
     assert library(300, 28672, dense)  # 112 column blocks x 3 row tiles > 256
-    assert library(256, 4096, union) and not library(255, 4096, union)
+    assert library(512, 4096, union) and not library(511, 4096, union) and not library(256, 28672, union)
+    assert library(300, 28672, union)
     assert not library(4096, 4112, dense) and not library(4096, 4112, union)
     # the union layout adds sigma, its chunk maxima and the row flags to the dense one
     assert lib.grinqh_workspace_bytes(2048, K, 6144, 8, union) > lib.grinqh_workspace_bytes(2048, K, 6144, 8, dense)

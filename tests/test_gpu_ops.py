@@ -285,10 +285,11 @@ def test_prefill_split_k(graded, dtype):
 @pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0]],
                          ids=["non_monotone", "skip_all", "all_planes", "tied"])
 def test_graded_prefill_grade_groups(t, dtype):
-    """The graded prefill consumes each scale group's rows ordered by zone set
-    (single-precision stages load and merge only their planes).  Zone sets
-    that are not prefixes, no active zone at all, every zone, and tied
-    thresholds must all give S10 within the weight-rounding bound."""
+    """The fused graded prefill (100 rows: the warp-specialised tile in fp16)
+    masks each row's inactive planes and adds its midpoint bias in the stage
+    store.  Zone sets that are not prefixes, no active zone at all, every
+    zone, and tied thresholds must all give S10 within the weight-rounding
+    bound."""
     from grinqh.kernel import grinqh_gemv_batch_union
     M, K, N, b = 100, 1024, 512, 8
     rng = np.random.default_rng(321)
@@ -342,15 +343,15 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
 @pytest.mark.parametrize("max_bits", [4, 8])
 @pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0], None],
                          ids=["non_monotone", "skip_all", "all_planes", "tied", "quantiles"])
-@pytest.mark.parametrize("M", [300, 512])
-def test_prefill_library_gemm_graded(M, t, max_bits, dtype):
-    """Graded (union) batches of 256 rows and more: the dequant kernel writes
+@pytest.mark.parametrize("M,K,N", [(512, 1056, 512), (300, 96, 22016)])
+def test_prefill_library_gemm_graded(M, K, N, t, max_bits, dtype):
+    """Graded (union) batches of 512 rows, and of 257-511 rows when the fused
+    grid would need more than one round (300 x 22016): the dequant kernel writes
     RNE(w_eff * s) from each row's zone set (inactive planes masked to zero,
     midpoint bias added), then the library GEMM.  Zone sets that are not
     prefixes, none, all, tied thresholds and the 70/20/8/2 % quantile mix, held
     to S10 within the weight-rounding bound, with bias."""
-    from grinqh.kernel import run_product
-    K, N = 1056, 512  # K % 64 == 32: the last dequant tile is half full
+    from grinqh.kernel import run_product  # K % 64 == 32: the last dequant tile is half full
     rng = np.random.default_rng(4321 + max_bits)
     W, x, s = _setup(rng, K, N, max_bits, dtype, M=M)
     if t is None:

@@ -47,7 +47,7 @@ void arm_kernel_timing() {
 }
 
 struct WorkspaceLayout {
-  size_t counter_off, sigma_off, perm_off, stage_off, xsort_off, partial_off, total;
+  size_t counter_off, sigma_off, partial_off, total;
   size_t wt_off, blas_off;  // library-GEMM prefill: dense weight [N][K], then the GEMM's workspace
   size_t chunk_off, flag_off;  // graded library-GEMM prefill: statistic partials, non-finite row flags
   bool library_gemm;
@@ -66,14 +66,13 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 }
 
 // [split-K counters (kCounterBytes, zero between calls) | sigma (K floats,
-// graded batches above kSigmaPrepassRows) | grade-grouped order of a graded
-// prefill (perm: K ints, stage zone sets: K/32 words, x in that order: M x K)
-// | split-K partials].  The counters sit at offset 0 for every shape, so a
-// workspace shared by calls of different shapes keeps them zero.
+// graded batches above kSigmaPrepassRows) | split-K partials].  The counters
+// sit at offset 0 for every shape, so a workspace shared by calls of
+// different shapes keeps them zero.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
   // [counters | graded: sigma, its chunk maxima, row flags | Wt | GEMM workspace]
-  if (M > kDecodeMaxRows && use_library_gemm(M, N, mode == GRINQH_MODE_UNION)) {
+  if (M > kDecodeMaxRows && use_library_gemm(M, N)) {
     const bool g = mode == GRINQH_MODE_UNION;
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.library_gemm = true;
@@ -94,13 +93,9 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
     partial = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
   }
   const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kSigmaPrepassRows;
-  const bool need_order = (mode == GRINQH_MODE_UNION) && M > kDecodeMaxRows;
   w.counter_off = 0;
   w.sigma_off = kCounterBytes;
-  w.perm_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
-  w.stage_off = w.perm_off + (need_order ? round_up((size_t)K * sizeof(int), 256) : 0);
-  w.xsort_off = w.stage_off + (need_order ? round_up((size_t)(K / 32) * sizeof(uint32_t), 256) : 0);
-  w.partial_off = w.xsort_off + (need_order ? round_up((size_t)M * (size_t)K * 2, 256) : 0);
+  w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
   return w;
 }
@@ -162,20 +157,11 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   p.sigma = nullptr;
   p.splits = prefill_splits(M, d.K, d.N);
   p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
-  if (graded) {  // batch statistic, then rows of each scale group ordered by zone set
+  if (graded) {  // the batch statistic the rows are graded on
     float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
-    int* perm = reinterpret_cast<int*>(ws + wl.perm_off);
-    uint32_t* stage_bits = reinterpret_cast<uint32_t*>(ws + wl.stage_off);
-    uint16_t* xsorted = reinterpret_cast<uint16_t*>(ws + wl.xsort_off);
-    int rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
-    if (rc == GRINQH_OK) rc = launch_grade_order(sigma, d.thr, d.K, d.gs, max_bits, perm, stage_bits, st);
-    if (rc == GRINQH_OK) rc = launch_permute_cols(xs, d.ldx, perm, (int)M, d.K, xsorted, st);
+    const int rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
     if (rc != GRINQH_OK) return rc;
     p.sigma = sigma;
-    p.perm = perm;
-    p.stage_bits = stage_bits;
-    p.x = xsorted;
-    p.ldx = d.K;
   }
   arm_kernel_timing();
   int splits_run = 1;

@@ -88,11 +88,6 @@ struct PrefillParams {
   int splits;            // grid.z: K ranges (1: y written directly)
   int stages_per_split;  // set by launch_prefill
   float* partial;        // [splits][M][N] fp32 when splits > 1 (the reduce kernel follows)
-  // graded, grade-grouped order (else nullptr): x holds the columns in this
-  // order, perm[k'] is the weight row of sorted position k' and
-  // stage_bits[k'/32] the zone-set union of each 32-row stage
-  const int* perm;
-  const uint32_t* stage_bits;
 };
 
 // Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.  p.splits
@@ -108,28 +103,26 @@ int prefill_block_rows(int64_t M, int64_t N);
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
 
-// Prefill from kLibraryGemmRows rows, graded from kLibraryGemmRowsGraded (and
-// N % 64 == 0): the weight Wt[N][K] = RNE(w * s) (graded: RNE(w_eff * s)
-// from the union statistic) is written once (dequant.hip), then a library
-// GEMM multiplies it (blas.hip); below, and for other N, the fused
-// dequantize-into-LDS kernel.  (Dense: at 256 rows the fused kernel was
-// faster for all four Llama-3-8B shapes, at 512 slower for three of them, at
-// 2048 rows 1.5-1.9x slower.  Graded: at 192 rows the fused kernel took 361 us
-// for the four shapes against 390, at 256 rows 392 against 379.)
+// Prefill from kLibraryGemmRows rows (and N % 64 == 0): the weight Wt[N][K] =
+// RNE(w * s) (graded: RNE(w_eff * s) from the union statistic) is written
+// once (dequant.hip), then a library GEMM multiplies it (blas.hip); below,
+// and for other N, the fused dequantize-into-LDS kernel.  (Dense: at 256 rows
+// the fused kernel was faster for all four Llama-3-8B shapes, at 512 slower
+// for three of them, at 2048 rows 1.5-1.9x slower; graded: 332 us fused
+// against 362 us for the four shapes at 256 rows, 557 against 421 at 512.)
 constexpr int64_t kLibraryGemmRows = 512;
-constexpr int64_t kLibraryGemmRowsGraded = 256;
-// Whether a prefill product takes the library path.  Dense batches of
-// 257-511 rows take it too when the fused kernel's grid of 128-row tiles
-// needs more than one round of blocks (it is then not split over K, and each
-// round runs the whole K): gate_up at 320 rows took 213 us fused, 141 us here,
-// while qkv, o_proj and down (at most 96 blocks) stay within 15 us either way.
-inline bool use_library_gemm(int64_t M, int64_t N, bool graded) {
+constexpr size_t kLibraryGemmWorkspace = size_t(128) << 20;  // hipBLASLt's stream-K algorithms ask up to ~60 MiB
+// Whether a prefill product takes the library path.  Batches of 257-511 rows
+// take it too when the fused kernel's grid of 128-row tiles needs more than
+// one round of blocks (it is then not split over K, and each round runs the
+// whole K): gate_up at 320 rows took 213 us fused, 141 us here (graded at 384
+// rows: 259 against 161), while qkv, o_proj and down (at most 96 blocks)
+// stay within 15 us either way.
+inline bool use_library_gemm(int64_t M, int64_t N) {
   if (N % 64 != 0) return false;
-  if (graded) return M >= kLibraryGemmRowsGraded;
   if (M >= kLibraryGemmRows) return true;
   return M > 256 && ((N / 16 + 15) / 16) * ((M + 127) / 128) > kTargetBlocks;
 }
-constexpr size_t kLibraryGemmWorkspace = size_t(128) << 20;  // hipBLASLt's stream-K algorithms ask up to ~60 MiB
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
                       int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st);
@@ -149,11 +142,6 @@ int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
               int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes, hipStream_t st);
 
-// Grade-grouped order of the graded prefill (grade_order.hip).
-int launch_grade_order(const float* sigma, const GradeThresholds& thr, int K, int gs, int max_bits, int* perm,
-                       uint32_t* stage_bits, hipStream_t st);
-int launch_permute_cols(const uint16_t* x, int64_t ldx, const int* perm, int M, int K, uint16_t* xs,
-                        hipStream_t st);
 
 // Benchmark timing of a product's main kernel: when armed (by
 // grinqh_time_next_product, for the calling thread's next product), the next

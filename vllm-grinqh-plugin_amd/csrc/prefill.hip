@@ -89,22 +89,6 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     uint16_t sraw[4 * JPT];  // scales of the stage's group when it starts a new group
     bool new_group;
   };
-  // Grade-grouped order (graded batches, p.perm set): the weight rows of a
-  // stage come from perm, and planes outside the union of their zone sets are
-  // not fetched (past-the-end offsets read 0).  The order of stage s+1 is
-  // fetched while stage s is loaded, so the plane loads never wait on it.
-  int rows_nx[RPT];
-  uint32_t planes_nx = (1u << Z) - 1u;
-  auto fetch_order = [&](int s) {
-    if constexpr (!DENSE) {
-      if (p.perm == nullptr || s >= s_end) return;
-      const int k0 = s * BK;
-#pragma unroll
-      for (int e = 0; e < RPT; ++e) rows_nx[e] = p.perm[k0 + rg * RPT + e];
-      planes_nx = p.stage_bits[k0 >> 5];
-      if (BK == 64) planes_nx |= p.stage_bits[(k0 >> 5) + 1];
-    }
-  };
   auto load_stage = [&](int s, Slot& L) {
     const int k0 = s * BK;
     L.new_group = (s == s_begin) || (k0 / p.gs != (k0 - BK) / p.gs);
@@ -122,30 +106,16 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + k0 + 8 * piece) * 2) : 0x80000000u;
       L.xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
-    if constexpr (DENSE) {
+    // every plane of the stage's rows; graded batches mask the inactive ones
+    // when the stage is stored (fetching only the active ones measured slower)
 #pragma unroll
-      for (int e = 0; e < RPT; ++e) {
-        const int row = k0 + rg * RPT + e;
-        const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
+    for (int e = 0; e < RPT; ++e) {
+      const int row = k0 + rg * RPT + e;
+      const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
 #pragma unroll
-        for (int z = 0; z < Z; ++z)
-          L.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
-      }
-    } else {
-      const bool grouped = p.perm != nullptr;
-      const uint32_t planes = planes_nx;
-#pragma unroll
-      for (int e = 0; e < RPT; ++e) {
-        const int row = grouped ? rows_nx[e] : k0 + rg * RPT + e;
-        const uint32_t rb = (uint32_t)row * plane_row_bytes + (uint32_t)wc_ld * 4u;
-#pragma unroll
-        for (int z = 0; z < Z; ++z) {
-          const uint32_t off = ((planes >> z) & 1u) ? rb + (uint32_t)z * p.NW * 4u : 0x80000000u;
-          L.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)off, 0, 0);
-        }
-        L.sig[e] = p.sigma[row];
-      }
-      fetch_order(s + 1);
+      for (int z = 0; z < Z; ++z)
+        L.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(prsrc, (int)(rb + (uint32_t)z * p.NW * 4u), 0, 0);
+      if constexpr (!DENSE) L.sig[e] = p.sigma[row];
     }
   };
 
@@ -270,7 +240,6 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     // exact) and are never stored.
     if (wave < NP / 64) {
       const int last = s_end - 1;
-      fetch_order(s_begin);
       load_stage(s_begin, LA);
       store_stage(0, LA);
       load_stage(min(s_begin + 1, last), LB);
@@ -297,7 +266,6 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     }
     multiply_stage((s - s_begin) & 1);
   } else if constexpr (PD == 1) {
-    fetch_order(s_begin);
     load_stage(s_begin, LA);
     store_stage(0, LA);
     __syncthreads();
@@ -313,7 +281,6 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     // two stages in flight: at the top of each iteration stage s is in LDS
     // buffer 0 and stage s+1 is loading into LB (a single-stage range loads
     // its stage twice, harmlessly)
-    fetch_order(s_begin);
     load_stage(s_begin, LA);
     store_stage(0, LA);
     load_stage(s + 1 < s_end ? s + 1 : s, LB);
@@ -425,19 +392,19 @@ int prefill_splits(int64_t M, int64_t K, int64_t N) {
 // wave), 32-row stages, one stage in flight (64-row stages or a second stage
 // do not fit 256 registers).  128-row tiles: fp16 dense batches run the
 // warp-specialised form (4 waves load and dequantize 32-row stages with two
-// stages in flight, 4 waves of 64 x 128 multiply), the others 8 waves of
-// 32 x 128 with 64-row stages (when K and the group size allow) and one stage
-// in flight.  Two waves per SIMD let one wave's dequantization and loads
-// overlap the other's MFMAs.
+// stages in flight, 4 waves of 64 x 128 multiply), dense or graded; bf16
+// runs 8 waves of 32 x 128 with 64-row stages (when K and the group size
+// allow) and one stage in flight.  Two waves per SIMD let one wave's
+// dequantization and loads overlap the other's MFMAs.
 struct PrefillShape {
   int bm, bk, pd;
 };
-static PrefillShape prefill_shape(const PrefillParams& p, int dtype, bool dense) {
+static PrefillShape prefill_shape(const PrefillParams& p, int dtype) {
   const bool bk64 = (p.K % 64 == 0) && (p.gs % 64 == 0);
   // (bf16's fp32 dequantization does not fit the 256-row tile's registers:
   // it always takes 128-row tiles)
   if (dtype == GRINQH_DTYPE_F16 && prefill_block_rows(p.M, p.N) == 256) return {256, 32, 1};
-  if (dtype == GRINQH_DTYPE_F16 && dense) return {128, 32, 2};
+  if (dtype == GRINQH_DTYPE_F16) return {128, 32, 2};
   return {128, bk64 ? 64 : 32, 1};
 }
 
@@ -462,7 +429,7 @@ int launch_prefill(const PrefillParams& p, int max_bits, int dtype, bool dense, 
                    int* splits_run) {
   if (!dense && p.sigma == nullptr) return GRINQH_ERR_INVALID;
   if (p.splits < 1 || (p.splits > 1 && p.partial == nullptr)) return GRINQH_ERR_INVALID;
-  const PrefillShape sh = prefill_shape(p, dtype, dense);
+  const PrefillShape sh = prefill_shape(p, dtype);
   *splits_run = prefill_splits_run(p, p.splits, sh.bk);
   const int Z = max_bits / 2;
   const int rc = dtype == GRINQH_DTYPE_BF16 ? launch_prefill_dt<BF16>(p, sh, Z, dense, st)
