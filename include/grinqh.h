@@ -87,12 +87,13 @@ int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, in
 /* Workspace needed by grinqh_gemm_or_gemv for this problem (0 if none): split-K
  * completion counters, fp32 split-K partial sums and, for union batches of
  * more than 16 rows, the per-row grading statistic.  From 512 rows (N a
- * multiple of 64; from 257 rows for N large enough that the fused kernel would
- * need two rounds of blocks) it also holds the dequantized weight (2*N*K
- * bytes) and 128 MiB for the library GEMM that multiplies it.  It must
- * be zero-filled once before its first use (every call leaves its counters
- * zero again; the rest needs no initial contents), 256-byte aligned, and calls
- * that share it must be ordered (same stream). */
+ * multiple of 64; from 224 rows, as bf16 batches take the library GEMM from
+ * there; from 257 rows for N large enough that the fused kernel would need
+ * two rounds of blocks) it also holds the dequantized weight (2*N*K bytes)
+ * that the library GEMM multiplies.  It must be zero-filled once before its
+ * first use (every call leaves its counters zero again; the rest needs no
+ * initial contents), 256-byte aligned, and calls that share it must be
+ * ordered (same stream). */
 size_t grinqh_workspace_bytes(int64_t M, int64_t K, int64_t N, int max_bits, int mode);
 
 /* The quantized linear y[M][N] = x[M][K] * W_eff (+ bias), x/scale/bias/y in `dtype`.

@@ -59,21 +59,23 @@ def test_workspace_query(lib):
 
 def test_workspace_query_library_gemm_path(lib):
     """The large-batch prefill path (dequantized weight + library GEMM) sizes
-    the workspace for the K-contiguous weight (2*N*K bytes) plus the GEMM's
-    128 MiB: from 512 rows, at 257-511 rows only when the fused grid would
-    need more than one round (gate_up's N), never when N / 16 is not a
-    multiple of 4; dense and union alike."""
-    K, gemm = 4096, 128 << 20
+    the workspace for the K-contiguous weight (2*N*K bytes) after the fused
+    kernel's regions (the GEMM itself takes no workspace).  The query has no dtype, so it
+    covers the path whenever either dtype may take it: from 512 rows, from
+    224 in bf16, at 257-511 rows when the fused grid would need more than one
+    round (gate_up's N); never when N / 16 is not a multiple of 4; dense and
+    union alike."""
+    K = 4096
     dense, union = 2, 1
-    library = lambda M, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode) >= 2 * N * K + gemm
-    assert library(512, 6144, dense) and library(2048, 28672, dense)
-    assert not library(511, 6144, dense) and not library(256, 28672, dense)
-    assert library(300, 28672, dense)  # 112 column blocks x 3 row tiles > 256
-    assert library(512, 4096, union) and not library(511, 4096, union) and not library(256, 28672, union)
-    assert library(300, 28672, union)
-    assert not library(4096, 4112, dense) and not library(4096, 4112, union)
+    library = lambda M, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode) >= 2 * N * K
+    for mode in (dense, union):
+        assert library(512, 6144, mode) and library(2048, 28672, mode) and library(300, 28672, mode)
+        assert library(224, 6144, mode) and not library(223, 6144, mode) and not library(128, 28672, mode)
+        assert not library(4096, 4112, mode)
     # the union layout adds sigma, its chunk maxima and the row flags to the dense one
     assert lib.grinqh_workspace_bytes(2048, K, 6144, 8, union) > lib.grinqh_workspace_bytes(2048, K, 6144, 8, dense)
+    # the fused kernel's split-K partials stay in front of the library regions
+    assert lib.grinqh_workspace_bytes(240, K, 4096, 8, dense) >= 2 * 4096 * K + 8 * 240 * 4096 * 4
 
 
 def test_invalid_arguments_rejected_on_host(lib):

@@ -48,8 +48,10 @@ void arm_kernel_timing() {
 
 struct WorkspaceLayout {
   size_t counter_off, sigma_off, partial_off, total;
-  size_t wt_off, blas_off;  // library-GEMM prefill: dense weight [N][K], then the GEMM's workspace
-  size_t chunk_off, flag_off;  // graded library-GEMM prefill: statistic partials, non-finite row flags
+  // library-GEMM prefill (when either dtype may take it): graded statistic
+  // partials and non-finite row flags, then the dense weight [N][K] -- after
+  // the regions the fused prefill uses
+  size_t chunk_off, flag_off, wt_off;
   bool library_gemm;
   DecodePlan plan;
 };
@@ -66,24 +68,14 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 }
 
 // [split-K counters (kCounterBytes, zero between calls) | sigma (K floats,
-// graded batches above kSigmaPrepassRows) | split-K partials].  The counters
-// sit at offset 0 for every shape, so a workspace shared by calls of
-// different shapes keeps them zero.
+// graded batches above kSigmaPrepassRows) | split-K partials | library-GEMM
+// regions].  The counters sit at offset 0 for every shape, so a workspace
+// shared by calls of different shapes keeps them zero.  The size does not
+// depend on the dtype: when either dtype may take the library path (bf16
+// from fewer rows) its regions follow those of the fused kernel, so either
+// path runs from the same workspace.
 WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   WorkspaceLayout w{};
-  // [counters | graded: sigma, its chunk maxima, row flags | Wt | GEMM workspace]
-  if (M > kDecodeMaxRows && use_library_gemm(M, N)) {
-    const bool g = mode == GRINQH_MODE_UNION;
-    const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
-    w.library_gemm = true;
-    w.sigma_off = kCounterBytes;
-    w.chunk_off = w.sigma_off + (g ? round_up((size_t)K * sizeof(float), 256) : 0);
-    w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
-    w.wt_off = w.flag_off + (g ? round_up((size_t)((K + 255) / 256) * (size_t)M, 256) : 0);
-    w.blas_off = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
-    w.total = w.blas_off + kLibraryGemmWorkspace;
-    return w;
-  }
   size_t partial = 0;
   if (M <= kDecodeMaxRows) {
     w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
@@ -92,11 +84,21 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
     const int splits = prefill_splits(M, K, N);
     partial = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
   }
-  const bool need_sigma = (mode == GRINQH_MODE_UNION) && M > kSigmaPrepassRows;
+  const bool g = mode == GRINQH_MODE_UNION;
+  const bool need_sigma = g && M > kSigmaPrepassRows;
   w.counter_off = 0;
   w.sigma_off = kCounterBytes;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
+  w.library_gemm = M > kDecodeMaxRows && (use_library_gemm(M, N, GRINQH_DTYPE_F16) ||
+                                          use_library_gemm(M, N, GRINQH_DTYPE_BF16));
+  if (w.library_gemm) {
+    const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
+    w.chunk_off = round_up(w.partial_off + partial, 256);
+    w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
+    w.wt_off = w.flag_off + (g ? round_up((size_t)((K + 255) / 256) * (size_t)M, 256) : 0);
+    w.total = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
+  }
   return w;
 }
 
@@ -119,7 +121,7 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // first reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
-  if (wl.library_gemm) {  // the (graded) weight once, then the library GEMM
+  if (wl.library_gemm && use_library_gemm(M, d.N, dtype)) {  // the (graded) weight once, then the library GEMM
     // an error a library left in this thread's last-error slot must not be
     // taken for a failure of the launches below
     (void)hipGetLastError();
@@ -134,7 +136,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, st);
     t_kernel_timing = KernelTiming{};
     if (rc == GRINQH_OK)
-      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, ws + wl.blas_off, kLibraryGemmWorkspace, st);
+      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, st);
     if (rc == GRINQH_OK && graded) {
       (void)hipGetLastError();  // the GEMM's library calls may leave one behind as well
       rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);

@@ -111,16 +111,22 @@ int prefill_splits(int64_t M, int64_t K, int64_t N);
 // for three of them, at 2048 rows 1.5-1.9x slower; graded: 332 us fused
 // against 362 us for the four shapes at 256 rows, 557 against 421 at 512.)
 constexpr int64_t kLibraryGemmRows = 512;
-constexpr size_t kLibraryGemmWorkspace = size_t(128) << 20;  // hipBLASLt's stream-K algorithms ask up to ~60 MiB
+// bf16 dequantizes in fp32 in the fused kernel, which makes it slower than in
+// fp16 (gate_up at 255 rows: 206 against 113 us): the four shapes took 418 us
+// fused and 319-328 us on the library path at 255 rows, 261 against 318 at
+// 128, and about even at 192 (where the library GEMM's choice for o_proj and
+// down is slow), hence the midpoint
+constexpr int64_t kLibraryGemmRowsBf16 = 224;
 // Whether a prefill product takes the library path.  Batches of 257-511 rows
 // take it too when the fused kernel's grid of 128-row tiles needs more than
 // one round of blocks (it is then not split over K, and each round runs the
 // whole K): gate_up at 320 rows took 213 us fused, 141 us here (graded at 384
 // rows: 259 against 161), while qkv, o_proj and down (at most 96 blocks)
 // stay within 15 us either way.
-inline bool use_library_gemm(int64_t M, int64_t N) {
+inline bool use_library_gemm(int64_t M, int64_t N, int dtype) {
   if (N % 64 != 0) return false;
   if (M >= kLibraryGemmRows) return true;
+  if (dtype == GRINQH_DTYPE_BF16 && M >= kLibraryGemmRowsBf16) return true;
   return M > 256 && ((N / 16 + 15) / 16) * ((M + 127) / 128) > kTargetBlocks;
 }
 // sigma == nullptr: dense; else graded with the union statistic sigma[K]
@@ -140,7 +146,7 @@ int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype,
 int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st);
 // y[M][N] = x[M][K] @ wt[N][K]^T (+ bias) in the activation dtype, fp32 accumulation
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
-              int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes, hipStream_t st);
+              int64_t N, int64_t K, int dtype, hipStream_t st);
 
 
 // Benchmark timing of a product's main kernel: when armed (by
