@@ -6,12 +6,17 @@ qkv 4096->6144, o_proj 4096->4096, gate_up 4096->28672, down 14336->4096 at
 M in {1, 4, 16, 64}; fp16 activations N(0,1) with 1 % of channels x20; weights
 0.02*N(0,1) RTN-quantised to int8 codes per 128-row group with fp16 scales;
 union grading with thresholds [0, P50, P80, P95] of sigma_k = max_m |x[m,k]|.
-One step = the 16 products once.  Weights rotate through enough copies to
-exceed 2x the 256 MB MALL, so timings reflect HBM.
+One step = the 16 products once.
+
+HBM-cold timing: every shape has a pool of weight copies of at least 2 GiB,
+handed out least recently used first, so that no timed product reads a weight
+copy that was read less than ~0.9 GB of weight traffic earlier (the MI355X
+MALL holds 256 MB).  The smallest distance actually seen between two reads
+of one copy, in bytes the products touched, is reported in ``config``.
 
 value = whole-step HBM throughput in algorithmic bytes (planes actually needed
 by the grading + scales + x + y) per second.  The JSON line also carries the
-per-case kernel times, the roofline of the dominant kernel, the prefill
+per-case product times, the roofline of the dominant kernel, the prefill
 TFLOP/s at M=2048 (dense, the reference's dispatch for M > 1), the graded
 prefill sweep of BASELINE configs[2] (M = 512, 2048, 8192, 70/20/8/2 % grade
 mix), the Llama-3-70B shapes of BASELINE configs[4] with every zone active
@@ -47,6 +52,7 @@ M_70B = (1, 64, 4096)
 GS = 128
 BITS = 8
 MALL_BYTES = 256 << 20
+POOL_BYTES = 2 << 30  # weight copies per shape: at least this many bytes
 
 
 def log(msg: str) -> None:
@@ -76,6 +82,59 @@ def synth_x(torch, M: int, K: int, seed: int, device):
 def thresholds_for(x, q=(0.5, 0.8, 0.95)):
     sigma = x.abs().float().amax(0).cpu().numpy()
     return [0.0] + [float(v) for v in np.quantile(sigma, q)]
+
+
+class ColdRotation:
+    """Least-recently-used hand-out of weight copies with exact accounting of
+    the bytes the products touch between two reads of one copy.
+
+    ``take(shape, touched)`` returns the next copy of ``shape`` (round robin
+    over its pool) for a product that touches ``touched`` bytes.  A graph
+    replays the takes made while it was captured, so after capturing a
+    sequence that is replayed cyclically, ``replay(takes)`` runs the same
+    sequence through the accounting once more: the distances it records are
+    the ones every timed replay sees, including the wrap from the end of the
+    sequence back to its start."""
+
+    def __init__(self, pools):
+        self.pools = pools
+        self.next = {k: 0 for k in pools}
+        self.clock = 0
+        self.last = {}
+        self.min_gap = None
+        self.log = None
+
+    def _use(self, key, touched):
+        if key in self.last:
+            gap = self.clock - self.last[key]
+            self.min_gap = gap if self.min_gap is None else min(self.min_gap, gap)
+        self.clock += touched
+        self.last[key] = self.clock
+
+    def take(self, shape, touched):
+        i = self.next[shape]
+        self.next[shape] = (i + 1) % len(self.pools[shape])
+        self._use((shape, i), touched)
+        if self.log is not None:
+            self.log.append(((shape, i), touched))
+        return self.pools[shape][i]
+
+    def record(self):
+        self.log = []
+
+    def stop(self):
+        takes, self.log = self.log, None
+        return takes
+
+    def replay(self, takes):
+        for key, touched in takes:
+            self._use(key, touched)
+
+
+def make_pool(base, nbytes_each: int, multiple: int = 4):
+    """``base`` plus clones: at least POOL_BYTES in all, a multiple of ``multiple`` copies."""
+    n = max(multiple, multiple * math.ceil(POOL_BYTES / (multiple * nbytes_each)))
+    return [base] + [tuple(t.clone() for t in base) for _ in range(n - 1)]
 
 
 def graph_time_us(torch, stream, call, n_it: int, replays: int = 3) -> float:
@@ -136,12 +195,17 @@ def traffic_for(kernel: str):
     return None
 
 
+def touched_bytes(rec) -> int:
+    """Weight bytes a product reads: the planes its grading needs and the scales."""
+    return rec["bytes"] - rec["M"] * rec["K"] * 2 - rec["M"] * rec["N"] * 2
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--reps", type=int, default=20, help="launches per case graph for kernel timing")
+    ap.add_argument("--reps", type=int, default=20, help="eager launches per case for the kernel-event timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B shape sweep (BASELINE configs[4])")
@@ -149,8 +213,8 @@ def main() -> int:
                     help="profiling run: one prefill product (e.g. gate_up:2048:union; MODE dense or union with "
                          "t = [0, P70, P90, P98]) twice as warm-up and twice counted; prints no JSON line")
     ap.add_argument("--pmc-pass", action="store_true",
-                    help="counter-collection run: each decode case twice (eager) and a 256 MiB copy kernel "
-                         "of known traffic for calibrating FETCH_SIZE / WRITE_SIZE; prints no JSON line")
+                    help="counter-collection run: each decode case twice (eager, cold weight copies) and a 256 MiB "
+                         "copy kernel of known traffic for calibrating FETCH_SIZE / WRITE_SIZE; prints no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only: the GRINQH hot path has no sharded path "
@@ -188,18 +252,16 @@ def main() -> int:
         log(f"prefill case {name} M={M} {mode}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s")
         return 0
 
-    # ---------------- weights (rotated copies to defeat the MALL)
-    base = {}
-    plane_bytes = 0
+    # ---------------- weights: a pool of >= POOL_BYTES of copies per shape, handed out LRU
+    pools = {}
     for i, (name, K, N) in enumerate(SHAPES):
         w, s = synth_weight(torch, K, N, 1000 + i, dev)
-        base[name] = (prepare_weight(w, BITS), s)
-        plane_bytes += base[name][0].numel() * 4 + s.numel() * 2
+        base = (prepare_weight(w, BITS), s)
         del w
-    n_copies = max(2, math.ceil(3 * MALL_BYTES / plane_bytes))
-    copies = {name: [base[name]] + [(p.clone(), s.clone()) for _ in range(n_copies - 1)]
-              for name, (p, s) in base.items()}
-    log(f"weights ready: {plane_bytes / 1e6:.1f} MB per copy x {n_copies} copies")
+        pools[name] = make_pool(base, base[0].numel() * 4 + s.numel() * 2)
+    rot = ColdRotation(pools)
+    copies_per_shape = {n: len(p) for n, p in pools.items()}
+    log("weight pools: " + ", ".join(f"{n} {len(p)} copies" for n, p in pools.items()))
 
     # ---------------- cases
     cases = []
@@ -209,25 +271,27 @@ def main() -> int:
             t = thresholds_for(x)
             zb, _ = grade(x, t, BITS)
             bits = np.unpackbits(zb.cpu().numpy()[:, None], axis=1).sum(1)
-            cases.append(dict(shape=name, K=K, N=N, M=M, x=x, t=t, bytes=decode_bytes(bits, K, N, M),
-                              mean_planes=float(bits.mean())))
+            c = dict(shape=name, K=K, N=N, M=M, x=x, t=t, bytes=decode_bytes(bits, K, N, M),
+                     mean_planes=float(bits.mean()))
+            c["touched"] = touched_bytes(c)
+            cases.append(c)
 
-    def call(c, r):
-        p, s = copies[c["shape"]][r]
+    def call(c):
+        p, s = rot.take(c["shape"], c["touched"])
         return run_product(c["x"], p, s, None, BITS, GS, c["N"] // 4, c["t"], "union")
 
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for c in cases:  # size the per-stream workspace before any capture
-            call(c, 0)
+            call(c)
     torch.cuda.synchronize()
 
     if args.pmc_pass:
         with torch.cuda.stream(stream):
             for c in cases:
                 for r in range(2):
-                    call(c, 1 + r)
+                    call(c)
                 torch.cuda.synchronize()
                 log(f"pmc pass: {c['shape']} M={c['M']} kernel {kernel_name(c['M'], BITS // 2)} "
                     f"bytes {c['bytes']}")
@@ -238,13 +302,17 @@ def main() -> int:
         log("pmc pass: calibration kernel (torch.neg, 256 MiB in, 256 MiB out) done")
         return 0
 
-    # per-case kernel time: graph of `reps` launches cycling the weight copies
+    # per-case product time: one graph of enough launches (cycling the shape's
+    # pool) that a copy is re-read only after >= 1 GiB of weight traffic
     for c in cases:
+        reps = max(args.reps, math.ceil((1 << 30) / c["touched"]))
         g = torch.cuda.CUDAGraph()
+        rot.record()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(g, stream=stream):
-                for j in range(args.reps):
-                    call(c, j % n_copies)
+                for _ in range(reps):
+                    call(c)
+        rot.replay(rot.stop())
         g.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -254,37 +322,43 @@ def main() -> int:
                 g.replay()
             e1.record(stream)
         e1.synchronize()
-        c["us"] = e0.elapsed_time(e1) * 1e3 / (3 * args.reps)
+        c["us"] = e0.elapsed_time(e1) * 1e3 / (3 * reps)
         c["gbs"] = c["bytes"] / (c["us"] * 1e-6) / 1e9
         log(f"{c['shape']:8s} M={c['M']:3d} planes/row={c['mean_planes']:.2f} {c['bytes'] / 1e6:7.2f} MB "
             f"{c['us']:8.2f} us {c['gbs']:8.1f} GB/s ({100 * c['gbs'] / HBM_PEAK_GBS:.1f}% HBM)")
         del g
 
-    # ---------------- the step: one graph per weight copy holding all 16 products
+    # ---------------- the step: graphs of the 16 products, each product on its
+    # own weight copy; enough graphs that every copy of the largest pool is
+    # used once per cycle of replays
+    n_graphs = max(len(p) for p in pools.values()) // len(DECODE_M)
     step_graphs = []
-    for r in range(n_copies):
+    rot.record()
+    for r in range(n_graphs):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(g, stream=stream):
                 for c in cases:
-                    call(c, r)
+                    call(c)
         step_graphs.append(g)
-    for i in range(args.warmup):
-        step_graphs[i % n_copies].replay()
+    rot.replay(rot.stop())
+    for i in range(max(args.warmup, n_graphs)):
+        step_graphs[i % n_graphs].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
         for i in range(args.steps):
-            step_graphs[i % n_copies].replay()
+            step_graphs[i % n_graphs].replay()
         e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = e0.elapsed_time(e1) / args.steps
     step_bytes = sum(c["bytes"] for c in cases)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"step {ms_per_step * 1e3:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s)")
+    log(f"step {ms_per_step * 1e3:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s, {n_graphs} step graphs)")
+    del step_graphs
 
     # ---------------- kernel timing: HIP events that the dispatch of each
     # product's main kernel records as the kernel starts and ends (the
@@ -300,13 +374,14 @@ def main() -> int:
     torch.cuda.synchronize()
     for c in cases:
         with torch.cuda.stream(stream):
-            for j, (a, b) in enumerate(ev_pairs):
+            for a, b in ev_pairs:
                 _lib.check(lib.grinqh_time_next_product(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event)),
                            "grinqh_time_next_product")
-                call(c, j % n_copies)
+                call(c)
         torch.cuda.synchronize()
         c["kernel_us"] = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in ev_pairs]))
         c["kernel"] = kernel_name(c["M"], BITS // 2)
+    decode_min_gap = rot.min_gap
     kernels = {}
     for c in cases:
         k = kernels.setdefault(c["kernel"], {"launches_per_step": 0, "bytes": 0, "us": 0.0})
@@ -329,15 +404,23 @@ def main() -> int:
     for k in kernels.values():
         del k["us"], k["bytes"]
 
+    def prefill_time_us(name, K, N, M, x, t, mode, n_it):
+        """Graph-timed product on rotated copies (every plane fetched counts as touched)."""
+        touched = K * N * BITS // 8 + (K // GS) * N * 2
+        n_it = max(n_it, math.ceil((1 << 30) / touched))  # a copy re-read after >= 1 GiB
+        rot.record()
+        us = graph_time_us(torch, stream, lambda j: run_product(
+            x, *rot.take(name, touched), None, BITS, GS, N // 4, t, mode), n_it)
+        rot.replay(rot.stop()[2:])  # the captured calls (the two eager sizing calls are not replayed)
+        return us
+
     # ---------------- prefill at M=2048 (dense dequantize-then-matmul, reference dispatch for M>1)
     prefill = None
     if not args.no_prefill:
         prefill = []
         for i, (name, K, N) in enumerate(SHAPES):
             x = synth_x(torch, PREFILL_M, K, 99 + i, dev)
-            cps = copies[name]
-            us = graph_time_us(torch, stream, lambda j: run_product(
-                x, cps[j % n_copies][0], cps[j % n_copies][1], None, BITS, GS, N // 4, [0.0] * 4, "dense"), 5)
+            us = prefill_time_us(name, K, N, PREFILL_M, x, [0.0] * 4, "dense", 5)
             tf = 2.0 * PREFILL_M * K * N / (us * 1e-6) / 1e12
             prefill.append({"shape": name, "M": PREFILL_M, "us": round(us, 2), "tflops": round(tf, 1),
                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
@@ -352,37 +435,42 @@ def main() -> int:
             for M in PREFILL_GRADED_M:
                 x = synth_x(torch, M, K, 199 + i, dev)
                 t = thresholds_for(x, (0.7, 0.9, 0.98))
-                cps = copies[name]
-                us = graph_time_us(torch, stream, lambda j: run_product(
-                    x, cps[j % n_copies][0], cps[j % n_copies][1], None, BITS, GS, N // 4, t, "union"), 3)
+                us = prefill_time_us(name, K, N, M, x, t, "union", 3)
                 tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
                 prefill_graded.append({"shape": name, "M": M, "us": round(us, 2), "tflops": round(tf, 1),
                                        "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
                 log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
                 del x
+    prefill_min_gap = rot.min_gap
+    del pools, rot
+    torch.cuda.empty_cache()
 
     # ---------------- Llama-3-70B shapes, adversarial grading (thresholds -1:
     # every token exceeds every threshold, so every plane is read); M <= 64 as GB/s, M = 4096 as TFLOP/s
     big = None
+    big_min_gap = None
     if not args.no_70b:
         big = []
         for i, (name, K, N) in enumerate(SHAPES_70B):
             w, s = synth_weight(torch, K, N, 2000 + i, dev)
-            p0 = prepare_weight(w, BITS)
+            base = (prepare_weight(w, BITS), s)
             del w
-            cps = [(p0, s), (p0.clone(), s.clone())]  # two copies of >= 168 MB rotate past the MALL
+            brot = ColdRotation({name: make_pool(base, base[0].numel() * 4 + s.numel() * 2, multiple=1)})
+            touched = K * N + (K // GS) * N * 2
             for M in M_70B:
                 x = synth_x(torch, M, K, 299 + i, dev)
                 t = [-1.0] * 4
-                n_it = 4
+                n_it = max(4, math.ceil((1 << 30) / touched))  # a copy re-read after >= 1 GiB
                 with torch.cuda.stream(stream):
-                    for j in range(2):
-                        run_product(x, cps[j][0], cps[j][1], None, BITS, GS, N // 4, t, "union")
+                    for _ in range(2):
+                        run_product(x, *brot.take(name, touched), None, BITS, GS, N // 4, t, "union")
                     torch.cuda.synchronize()
                     g = torch.cuda.CUDAGraph()
+                    brot.record()
                     with torch.cuda.graph(g, stream=stream):
-                        for j in range(n_it):
-                            run_product(x, cps[j % 2][0], cps[j % 2][1], None, BITS, GS, N // 4, t, "union")
+                        for _ in range(n_it):
+                            run_product(x, *brot.take(name, touched), None, BITS, GS, N // 4, t, "union")
+                    brot.replay(brot.stop())
                     g.replay()
                     torch.cuda.synchronize()
                     e0.record(stream)
@@ -402,33 +490,61 @@ def main() -> int:
                     log(f"70B {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
                 big.append(rec)
                 del g, x
-            del cps, p0, s
+            gap = brot.min_gap
+            big_min_gap = gap if big_min_gap is None or (gap is not None and gap < big_min_gap) else big_min_gap
+            del brot, base, s
             torch.cuda.empty_cache()
 
-    # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores
+    # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores, over the
+    # whole decode sweep (graded union math), plus its dense dispatch (S9) at 16 rows
     cpu = None
     if not args.no_cpu_baseline:
         from oracle import cpu_reference
         cores = len(os.sched_getaffinity(0))
         torch.set_num_threads(cores)
-        sample = [c for c in cases if c["M"] == 1]
-        tot_b, tot_t = 0, 0.0
-        for c in sample:
-            p, s = copies[c["shape"]][0]
-            pc, sc, xc = p.cpu(), s.cpu(), c["x"].cpu()
-            cpu_reference.graded(xc, pc, sc, c["t"], GS, BITS)  # warmup
-            ts = []
-            for _ in range(3):
-                t0 = time.perf_counter()
+        w_host = {}
+        for i, (name, K, N) in enumerate(SHAPES):
+            w, s = synth_weight(torch, K, N, 1000 + i, dev)
+            w_host[name] = (prepare_weight(w, BITS).cpu(), s.cpu())
+            del w
+        xs = [(c, c["x"].cpu()) for c in cases]
+
+        def sweep():
+            for c, xc in xs:
+                pc, sc = w_host[c["shape"]]
                 cpu_reference.graded(xc, pc, sc, c["t"], GS, BITS)
+
+        def dense16():
+            for c, xc in xs:
+                if c["M"] == 16:
+                    pc, sc = w_host[c["shape"]]
+                    cpu_reference.dense_prefill(xc, pc, sc, GS, BITS)
+
+        def median_time(fn, runs=5):
+            fn()  # warm-up
+            ts = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                fn()
                 ts.append(time.perf_counter() - t0)
-            tot_t += float(np.median(ts))
-            tot_b += c["bytes"]
-        cpu = {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-               "sample": "graded union math of the reference (masked fp32 weights + matmul, torch CPU eager) on the "
-                         "four decode shapes at M=1, median of 3 after 1 warmup",
+            return float(np.median(ts))
+
+        t_sweep = median_time(sweep)
+        t_dense = median_time(dense16)
+        dense_bytes = sum(c["K"] * c["N"] + (c["K"] // GS) * c["N"] * 2 + c["M"] * (c["K"] + c["N"]) * 2
+                          for c in cases if c["M"] == 16)
+        cpu = {"value": round(step_bytes / t_sweep / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": "the whole decode sweep (16 products) in the reference's graded union math (masked fp32 "
+                         "weights + matmul, torch CPU eager), median of 5 after 1 warm-up",
+               "ms_per_step": round(t_sweep * 1e3, 1),
+               "dense_s9_m16": {"value": round(dense_bytes / t_dense / 1e9, 3), "unit": "GB/s",
+                                "sample": "the reference's dense dispatch for more than one row (unpack, sign "
+                                          "extend, postshuffle, x.dtype scale, matmul) on the four shapes at "
+                                          "M=16, all planes, median of 5 after 1 warm-up",
+                                "ms": round(t_dense * 1e3, 1)},
                "cpu": _cpu_model()}
-        log(f"cpu baseline {cpu['value']} GB/s on {cores} cores")
+        log(f"cpu baseline {cpu['value']} GB/s on {cores} cores ({t_sweep * 1e3:.0f} ms per step); dense S9 "
+            f"M=16 {cpu['dense_s9_m16']['value']} GB/s")
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -436,12 +552,15 @@ def main() -> int:
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "decode sweep (BASELINE configs[1]): Llama-3-8B qkv/o_proj/gate_up/down x "
                                "M=1,4,16,64, union grading t=[0,P50,P80,P95], max_bits 8, group 128",
-                   "weight_copies": n_copies, "frac_of_hbm_roofline": round(value / HBM_PEAK_GBS, 4)},
+                   "weight_copies": copies_per_shape,
+                   "min_bytes_between_rereads": {"decode": decode_min_gap, "prefill": prefill_min_gap,
+                                                 "llama70b": big_min_gap},
+                   "frac_of_hbm_roofline": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,
-        "cases": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in c.items() if k not in ("x", "t")}
-                  for c in cases],
+        "cases": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in c.items()
+                   if k not in ("x", "t", "touched")} for c in cases],
         "prefill": prefill,
         "prefill_graded": prefill_graded,
         "llama70b_adversarial": big,

@@ -270,6 +270,41 @@ def dense_weight(w_int8: np.ndarray, scale: np.ndarray, group_size: int, dtype: 
     return rne_cast(w_int8.astype(np.float64) * s, dtype)
 
 
+def graded_weight_rounded(w_int8: np.ndarray, zone_bits: np.ndarray, scale: np.ndarray, max_bits: int,
+                          group_size: int, dtype: str) -> np.ndarray:
+    """``RNE_dtype(w_eff[k,n] * scale[k//gs,n])``: the S7 effective weight scaled
+    and rounded once to the activation dtype, the way S9 rounds the dense weight
+    (grinqh/kernel.py:578-586).  With every zone active it is ``dense_weight``.
+    This is the weight a graded kernel multiplies when it applies the scale
+    before the matmul instead of after it (the reference's S10 keeps
+    ``x * w_eff`` and the scale in fp32, grinqh/kernel.py:321-344)."""
+    K = w_int8.shape[0]
+    weff = effective_weight(w_int8, zone_bits, max_bits).astype(np.float64)
+    s = rne_cast(_scale_rows(scale, K, group_size), dtype)
+    with np.errstate(over="ignore"):
+        return rne_cast(weff * s, dtype)
+
+
+def gemv_union_rounded_f64(x: np.ndarray, w_int8: np.ndarray, scale: np.ndarray, thresholds, max_bits: int,
+                           group_size: int, dtype: str) -> np.ndarray:
+    """S10 with the scaled effective weight rounded to the activation dtype
+    before the product: ``x @ graded_weight_rounded(...)`` in float64, grading
+    on the union statistic (grinqh/kernel.py:249-289)."""
+    x = np.asarray(x, dtype=np.float64)
+    sigma = np.fmax.reduce(np.abs(x), axis=0)
+    bits = grade(sigma, thresholds, max_bits)
+    return x @ graded_weight_rounded(w_int8, bits, scale, max_bits, group_size, dtype)
+
+
+def dense_exact_f64(x, w_int8, scale, group_size) -> np.ndarray:
+    """Dense product with the scale kept exact (``x @ (W * s)`` in float64, no
+    rounding of ``W*s``): S10 with every zone active (tests/test_grinqh_ops.py:170,
+    190), what a kernel that applies the scale in fp32 computes for the
+    dense dispatch."""
+    x = np.asarray(x, dtype=np.float64)
+    return x @ (w_int8.astype(np.float64) * _scale_rows(scale, w_int8.shape[0], group_size))
+
+
 def dense_prefill_f64(x, w_int8, scale, group_size, dtype="float16") -> np.ndarray:
     """S9 product in float64 before the output cast: ``X @ Wd`` (grinqh/kernel.py:587)."""
     return np.asarray(x, dtype=np.float64) @ dense_weight(w_int8, scale, group_size, dtype)

@@ -2,6 +2,9 @@
 output tolerance used by every floating-point parity check."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -29,20 +32,6 @@ def dense_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, dtype:
     u = UNIT_ROUNDOFF[dtype]
     s = np.repeat(np.abs(np.asarray(scale, dtype=np.float64)), group_size, axis=0)[: W.shape[0]]
     return u * (np.abs(np.asarray(x, dtype=np.float64)) @ (np.abs(W.astype(np.float64)) * s))
-
-
-def graded_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, thresholds, max_bits: int, dtype: str,
-                          group_size: int = 128):
-    """The same bound for a union-graded product whose kernel rounds the
-    effective weight w_eff*s to the activation dtype (the prefill kernel for
-    batches above 64 rows): u * (|x| @ |w_eff*s|), w_eff from the union grade."""
-    from oracle import grinqh_oracle as O
-    u = UNIT_ROUNDOFF[dtype]
-    xa = np.abs(np.asarray(x, dtype=np.float64))
-    sigma = np.abs(np.asarray(x, dtype=np.float32)).max(0)
-    weff = O.effective_weight(W, O.grade(sigma, thresholds, max_bits), max_bits).astype(np.float64)
-    s = np.repeat(np.abs(np.asarray(scale, dtype=np.float64)), group_size, axis=0)[: W.shape[0]]
-    return u * (xa @ (np.abs(weff) * s))
 
 
 def output_tolerance(ref_pre: np.ndarray, dtype: str, bias=None) -> np.ndarray:
@@ -82,3 +71,34 @@ def assert_output_close(y: torch.Tensor, ref_pre: np.ndarray, ref_final: np.ndar
                            f"max abs err {stats['max_abs']:.3e}, worst excess "
                            f"{float((err[ok] - tol[ok]).max()):.3e}")
     return stats
+
+
+def error_stats(y, ref_final: np.ndarray) -> dict:
+    """Max abs error, max rel error (outputs with |ref| >= 1 % of rms(ref)) and
+    max abs error / rms(ref) of a kernel output against a reference output."""
+    got = (y.detach().float().cpu().double().numpy() if isinstance(y, torch.Tensor) else np.asarray(y, np.float64))
+    ref = np.asarray(ref_final, dtype=np.float64)
+    got = got.reshape(ref.shape)
+    ok = np.isfinite(ref)
+    if not ok.any():
+        return {"max_abs": 0.0, "max_rel": 0.0, "max_abs_over_rms": 0.0, "rms": 0.0}
+    err = np.abs(got[ok] - ref[ok])
+    r = np.abs(ref[ok])
+    rms = float(np.sqrt(np.mean(r ** 2)))
+    big = r >= 0.01 * rms
+    return {"max_abs": float(err.max()),
+            "max_rel": float((err[big] / r[big]).max()) if big.any() else 0.0,
+            "max_abs_over_rms": float(err.max() / rms) if rms > 0 else 0.0,
+            "rms": rms}
+
+
+def record_errors(config: str, case: str, **fields) -> None:
+    """Append one error record (JSON line) to the file named by the
+    GRINQH_PARITY_LOG environment variable, if set; tests/parity_report.py
+    turns these records into the per-config error table."""
+    path = os.environ.get("GRINQH_PARITY_LOG")
+    if not path:
+        return
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "a") as f:
+        f.write(json.dumps({"config": config, "case": case, **fields}) + "\n")

@@ -104,3 +104,23 @@ def test_invalid_arguments_rejected_on_host(lib):
     assert lib.grinqh_pack_planes(None, None, 4, 20, 8, None) == INVALID
     assert lib.grinqh_unpack_planes(None, None, 1, None, 4, 32, 5, None) == INVALID
     assert lib.grinqh_grade(None, 1, 32, 32, 0, 3, t, None, None, None) == INVALID
+
+
+def test_activations_beyond_32_bit_offsets_rejected(lib):
+    """Kernels that address x through 32-bit buffer offsets refuse an x of
+    2 GiB or more instead of reading wrong rows: the fused prefill (taken at
+    every batch size when N/16 is not a multiple of 4) for the whole batch,
+    the GEMV / decode kernels for the rows of one launch."""
+    from grinqh import _lib
+    t = _lib.thresholds_f32([0.0] * 4)
+    dummy = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    ws = ctypes.c_void_p(1 << 20)
+
+    def call(M, K, ldx, N):
+        return lib.grinqh_gemm_or_gemv(dummy, M, K, ldx, N, 0, dummy, dummy, None, dummy, 2, 128, t,
+                                       _lib.MODE_DENSE, ws, 1 << 40, None)
+
+    # fused prefill: 2^31 bytes of x (N = 48: N/16 = 3, never the library path)
+    assert call(1 << 18, 4096, 4096, 48) == _lib.GRINQH_ERR_INVALID
+    # one decode launch: 2 rows of 2^30 halves each
+    assert call(2, 32, 1 << 30, 48) == _lib.GRINQH_ERR_INVALID

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import grinqh_oracle as O
-from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound, graded_rounding_bound,
+from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound,
                             rand_weight, to_dtype_np)
 
 pytestmark = pytest.mark.gpu
@@ -47,11 +47,23 @@ def _prepare(W, b):
 
 
 def rounds_weight(M, dtype):
-    """Whether the kernel serving an M-row graded batch rounds w_eff*s to the
-    activation dtype (as the reference's dense path does) instead of applying
-    the scale in fp32: the prefill kernel above 64 rows, and the fp16 decode
-    kernel for 17-64 rows."""
+    """Whether the kernel serving an M-row batch rounds w_eff*s to the
+    activation dtype (as the reference's dense path does, grinqh/kernel.py:586)
+    instead of applying the scale in fp32 after the sum: the prefill kernels
+    above 64 rows, and the fp16 decode kernel for 17-64 rows."""
     return M > 64 or (M > 16 and dtype == "float16")
+
+
+def own_product(x, W, s, t, b, gs, dtype, graded):
+    """Float64 product the kernel serving this batch computes: S10 (graded) or
+    the exact dense product when it applies the scale after the sum, the same
+    with RNE(w_eff*s) -- S9 for the dense dispatch -- when it rounds the
+    scaled weight first.  Kernels are held to it with the base tolerance."""
+    M = np.asarray(x).reshape(-1, W.shape[0]).shape[0]
+    if rounds_weight(M, dtype):
+        return (O.gemv_union_rounded_f64(x, W, s, t, b, gs, dtype) if graded
+                else O.dense_prefill_f64(x, W, s, gs, dtype))
+    return O.gemv_union_f64(x, W, s, t, b, gs) if graded else O.dense_exact_f64(x, W, s, gs)
 
 
 def _tdt(x, dtype):
@@ -146,8 +158,11 @@ def test_dense_prefill_matches_reference(max_bits, dtype):
     rng = np.random.default_rng(50 + max_bits)
     W, x, s = _setup(rng, 384, 320, max_bits, dtype, M=16)
     y = grinqh_prefill_dense(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), 128, 80, max_bits)
+    own = own_product(x, W, s, None, max_bits, 128, dtype, graded=False)
+    assert_output_close(y, own, O.bias_add(own, None, dtype), dtype, what="dense prefill")
+    # against S9 itself (W*s rounded by the reference, kept exact here): within that rounding
     pre = O.dense_prefill_f64(x, W, s, 128, dtype)
-    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="dense prefill",
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="dense prefill vs S9",
                         extra_tol=dense_rounding_bound(x, W, s, dtype))
 
 
@@ -227,12 +242,8 @@ def test_union_graded_batches(M, max_bits, dtype):
     sigma = np.abs(x).max(0).astype(np.float32)
     t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), None, max_bits, 128, 192, t)
-    pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
-    # the prefill kernel (above 64 rows) and the fp16 17-64-row decode kernel
-    # round w_eff*s to the activation dtype before multiplying
-    extra = graded_rounding_bound(x, W, s, t, max_bits, dtype) if rounds_weight(M, dtype) else None
-    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, max_bits, 128, dtype), dtype, what=f"union M={M}",
-                        extra_tol=extra)
+    own = own_product(x, W, s, t, max_bits, 128, dtype, graded=True)
+    assert_output_close(y, own, O.bias_add(own, None, dtype), dtype, what=f"union M={M}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -250,7 +261,7 @@ def test_prefill_dense_shapes(M, K, N, max_bits, dtype):
                     N // 4, [0.0] * 4, "dense")
     pre = O.dense_prefill_f64(x, W, s, 128, dtype)
     assert_output_close(y, pre, O.dense_prefill(x, W, s, bias, 128, dtype), dtype, bias=bias,
-                        what=f"prefill {M}x{K}x{N}", extra_tol=dense_rounding_bound(x, W, s, dtype))
+                        what=f"prefill {M}x{K}x{N}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -269,16 +280,14 @@ def test_prefill_split_k(graded, dtype):
         sigma = np.abs(x).max(0).astype(np.float32)
         t = [0.0] + np.quantile(sigma, [0.7, 0.9, 0.98]).tolist()
         y = run_product(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128, N // 4, t, "union")
-        pre = O.gemv_union_f64(x, W, s, t, b, 128)
-        fin = O.gemv_union(x, W, s, bias, t, b, 128, dtype)
-        extra = graded_rounding_bound(x, W, s, t, b, dtype)
+        pre = O.gemv_union_rounded_f64(x, W, s, t, b, 128, dtype)
+        fin = O.bias_add(pre, bias, dtype)
     else:
         y = run_product(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128, N // 4,
                         [0.0] * 4, "dense")
         pre = O.dense_prefill_f64(x, W, s, 128, dtype)
         fin = O.dense_prefill(x, W, s, bias, 128, dtype)
-        extra = dense_rounding_bound(x, W, s, dtype)
-    assert_output_close(y, pre, fin, dtype, bias=bias, what=f"split-K prefill graded={graded}", extra_tol=extra)
+    assert_output_close(y, pre, fin, dtype, bias=bias, what=f"split-K prefill graded={graded}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -295,9 +304,8 @@ def test_graded_prefill_grade_groups(t, dtype):
     rng = np.random.default_rng(321)
     W, x, s = _setup(rng, K, N, b, dtype, M=M)
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), None, b, 128, N // 4, t)
-    pre = O.gemv_union_f64(x, W, s, t, b, 128)
-    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, b, 128, dtype), dtype, what=f"grade groups t={t}",
-                        extra_tol=graded_rounding_bound(x, W, s, t, b, dtype))
+    pre = O.gemv_union_rounded_f64(x, W, s, t, b, 128, dtype)
+    assert_output_close(y, pre, O.bias_add(pre, None, dtype), dtype, what=f"grade groups t={t}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -312,8 +320,7 @@ def test_prefill_256_row_tiles(dtype):
     W, x, s = _setup(rng, K, N, 8, dtype, M=M)
     y = grinqh_prefill_dense(_tdt(x, dtype), _prepare(W, 8), _tdt(s, dtype), 128, N // 4, 8)
     pre = O.dense_prefill_f64(x, W, s, 128, dtype)
-    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="prefill 256-row tiles",
-                        extra_tol=dense_rounding_bound(x, W, s, dtype))
+    assert_output_close(y, pre, O.dense_prefill(x, W, s, None, 128, dtype), dtype, what="prefill 256-row tiles")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -336,7 +343,7 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
                     N // 4, [0.0] * 4, "dense")
     pre = O.dense_prefill_f64(x, W, s, 128, dtype)
     assert_output_close(y, pre, O.dense_prefill(x, W, s, bias, 128, dtype), dtype, bias=bias,
-                        what=f"library prefill {M}x{K}x{N}", extra_tol=dense_rounding_bound(x, W, s, dtype))
+                        what=f"library prefill {M}x{K}x{N}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -360,10 +367,9 @@ def test_prefill_library_gemm_graded(M, K, N, t, max_bits, dtype):
     bias = to_dtype_np(rng.standard_normal(N), dtype)
     y = run_product(_tdt(x, dtype), _prepare(W, max_bits), _tdt(s, dtype), _tdt(bias, dtype), max_bits, 128,
                     N // 4, t, "union")
-    pre = O.gemv_union_f64(x, W, s, t, max_bits, 128)
-    assert_output_close(y, pre, O.gemv_union(x, W, s, bias, t, max_bits, 128, dtype), dtype, bias=bias,
-                        what=f"library graded prefill t={t}",
-                        extra_tol=graded_rounding_bound(x, W, s, t, max_bits, dtype))
+    pre = O.gemv_union_rounded_f64(x, W, s, t, max_bits, 128, dtype)
+    assert_output_close(y, pre, O.bias_add(pre, bias, dtype), dtype, bias=bias,
+                        what=f"library graded prefill t={t}")
 
 
 @pytest.mark.parametrize("mode,M,K,N", [("dense", 512, 2048, 1024), ("union", 512, 2048, 1024),
@@ -372,8 +378,10 @@ def test_prefill_library_gemm_graded(M, K, N, t, max_bits, dtype):
 def test_graph_capture_library_prefill(mode, M, K, N):
     """A library-path product (dequant kernel, library GEMM, graded row pass)
     captured in a HIP graph and replayed several times with eager work in
-    between matches the eager result on every replay.  The gate_up shape at
-    2048 rows takes the library's stream-K GEMM, which uses its workspace."""
+    between matches the eager result on every replay.  The GEMM is given no
+    workspace: with one, a captured gate_up product at 2048 rows (a stream-K
+    kernel using that workspace) once gave a wrong result on a later replay,
+    for a reason not established; this checks the configuration in use."""
     from grinqh.kernel import run_product
     rng = np.random.default_rng(88)
     W, x, s = _setup(rng, K, N, 8, "float16", M=M, scale_sd=0.01)
@@ -415,7 +423,7 @@ def test_prefill_library_gemm_70b_qkv_shape(mode):
     xs = x[:R]
     assert_output_close(y[:R], O.dense_prefill_f64(xs, W, s, 128, "float16"),
                         O.dense_prefill(xs, W, s, None, 128, "float16"), "float16",
-                        what=f"70B qkv M={M} {mode}", extra_tol=dense_rounding_bound(xs, W, s, "float16"))
+                        what=f"70B qkv M={M} {mode}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -436,8 +444,7 @@ def test_prefill_library_gemm_strided_rows(dtype):
     fin = O.dense_prefill(x, W, s, None, 128, dtype)
     for _ in range(2):
         y = run_product(xt, P, st, None, b, 128, N // 4, [0.0] * 4, "dense")
-        assert_output_close(y, pre, fin, dtype, what="library prefill, strided rows",
-                            extra_tol=dense_rounding_bound(x, W, s, dtype))
+        assert_output_close(y, pre, fin, dtype, what="library prefill, strided rows")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -453,10 +460,13 @@ def test_reference_dispatch_dense_batches(M, dtype):
     y = torch.ops.grinqh.gemm_or_gemv(_tdt(x3, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128,
                                       128, [5.0] * 4)
     assert y.shape == (1, M, 512) and y.dtype == TORCH_DTYPES[dtype]
-    pre = O.dense_prefill_f64(x, W, s, 128, dtype)
-    fin = O.dense_prefill(x, W, s, bias, 128, dtype)
-    assert_output_close(y.reshape(M, 512), pre, fin, dtype, bias=bias, what="dense dispatch",
-                        extra_tol=dense_rounding_bound(x, W, s, dtype))
+    own = own_product(x, W, s, None, b, 128, dtype, graded=False)
+    assert_output_close(y.reshape(M, 512), own, O.bias_add(own, bias, dtype), dtype, bias=bias,
+                        what="dense dispatch")
+    if not rounds_weight(M, dtype):  # against S9 itself: within the reference's rounding of W*s
+        pre = O.dense_prefill_f64(x, W, s, 128, dtype)
+        assert_output_close(y.reshape(M, 512), pre, O.dense_prefill(x, W, s, bias, 128, dtype), dtype, bias=bias,
+                            what="dense dispatch vs S9", extra_tol=dense_rounding_bound(x, W, s, dtype))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -476,10 +486,8 @@ def test_llama_shapes_graded(shape, M, dtype):
     sigma = np.abs(x).max(0).astype(np.float32)
     t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, 8), _tdt(s, dtype), None, 8, 128, N // 4, t)
-    pre = O.gemv_union_f64(x, W, s, t, 8, 128)
-    extra = graded_rounding_bound(x, W, s, t, 8, dtype) if rounds_weight(M, dtype) else None
-    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, 8, 128, dtype), dtype, what=f"{shape} M={M}",
-                        extra_tol=extra)
+    own = own_product(x, W, s, t, 8, 128, dtype, graded=True)
+    assert_output_close(y, own, O.bias_add(own, None, dtype), dtype, what=f"{shape} M={M}")
 
 
 def test_split_k_is_deterministic():
@@ -536,10 +544,8 @@ def test_decode_short_k_ranges(K, M, dtype):
     sigma = np.abs(x).max(0).astype(np.float32)
     t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
     y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), None, b, gs, N // 4, t)
-    pre = O.gemv_union_f64(x, W, s, t, b, gs)
-    extra = graded_rounding_bound(x, W, s, t, b, dtype, group_size=gs) if rounds_weight(M, dtype) else None
-    assert_output_close(y, pre, O.gemv_union(x, W, s, None, t, b, gs, dtype), dtype, what=f"K={K} M={M}",
-                        extra_tol=extra)
+    own = own_product(x, W, s, t, b, gs, dtype, graded=True)
+    assert_output_close(y, own, O.bias_add(own, None, dtype), dtype, what=f"K={K} M={M}")
 
 
 @pytest.mark.parametrize("mode", ["union", "dense"])
@@ -562,16 +568,13 @@ def test_large_scales_round_once(M, mode):
         sigma = np.abs(x).max(0).astype(np.float32)
         t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
         y = grinqh_gemv_batch_union(xt, P, st, None, b, 128, N // 4, t)
-        pre = O.gemv_union_f64(x, W, s, t, b, 128)
-        fin = O.gemv_union(x, W, s, None, t, b, 128, dtype)
-        extra = graded_rounding_bound(x, W, s, t, b, dtype)
+        pre = own_product(x, W, s, t, b, 128, dtype, graded=True)
     else:
         y = grinqh_prefill_dense(xt, P, st, 128, N // 4, b)
         pre = O.dense_prefill_f64(x, W, s, 128, dtype)
-        fin = O.dense_prefill(x, W, s, None, 128, dtype)
-        extra = dense_rounding_bound(x, W, s, dtype)
+    fin = O.bias_add(pre, None, dtype)
     assert np.isfinite(fin).all()
-    assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}", extra_tol=extra)
+    assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -636,3 +639,37 @@ def test_graph_capture_replay_matches_eager():
         assert torch.equal(yg, eager), f"replay {i}"
         _ = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, 1024, t)
         torch.cuda.synchronize()
+
+
+def test_graph_survives_workspace_growth():
+    """A graph captured while the stream's workspace was small keeps writing
+    into that buffer on every replay; growing the workspace afterwards (an
+    eager call of a larger batch on the same stream) must not free it.  The
+    replay after the growth matches the eager result, and the tensors
+    allocated in between are untouched."""
+    from grinqh.kernel import grinqh_gemv_batch_union, run_product
+    rng = np.random.default_rng(12)
+    K, N = 4096, 4096
+    W, x, s = _setup(rng, K, N, 8, "float16", M=16, scale_sd=0.01)
+    P, st = _prepare(W, 8), _tdt(s, "float16")
+    xin = _tdt(x, "float16")
+    t = [0.0, 0.5, 1.0, 2.0]
+    s_cap = torch.cuda.Stream()  # a fresh stream: its workspace starts at the size of this batch
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        eager = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, N // 4, t).clone()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s_cap):
+            yg = grinqh_gemv_batch_union(xin, P, st, None, 8, 128, N // 4, t)
+        big = _tdt(rng.standard_normal((512, K)), "float16")
+        run_product(big, P, st, None, 8, 128, N // 4, [0.0] * 4, "dense")  # grows the workspace (library path)
+        torch.cuda.synchronize()
+        canary = [torch.full((1 << 20,), 7.0, device="cuda") for _ in range(64)]  # reuse of freed memory
+    torch.cuda.current_stream().wait_stream(s_cap)
+    for i in range(3):
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, eager), f"replay {i} after the workspace grew"
+    assert all(bool((c == 7.0).all()) for c in canary), "a replay wrote into memory freed by the growth"

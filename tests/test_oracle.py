@@ -273,3 +273,68 @@ def test_dispatch_shapes():
     np.testing.assert_array_equal(y.reshape(6, 64), O.dense_prefill(x.reshape(6, 128), W, s, None, 128))
     y1 = O.gemm_or_gemv(x[:1, :1], W, s, None, 8, 128, [0.1] * 4)
     np.testing.assert_array_equal(y1.reshape(1, 64), O.gemv(x[0, :1], W, s, None, [0.1] * 4, 8, 128))
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("b", BITS)
+def test_graded_weight_rounded_against_torch(dtype, b):
+    """RNE(w_eff * s): the effective integer weight (already pinned above) times
+    the scale in fp32 -- exact, since |w_eff| < 2^9 and s has at most 11
+    significant bits -- then torch's own cast to the activation dtype.  With
+    every zone active it equals S9's dense weight."""
+    rng = np.random.default_rng(13 + b)
+    K, N = 256, 96
+    W = _rand_w(rng, K, N, b)
+    tdt = torch.float16 if dtype == "float16" else torch.bfloat16
+    s = torch.from_numpy(rng.standard_normal((2, N)).astype(np.float32) * 3).to(tdt)
+    x = rng.standard_normal(K).astype(np.float32)
+    t = [0.3, 0.9, 1.4, 2.2]
+    bits = O.grade(x, t, b)
+    weff = torch.from_numpy(O.effective_weight(W, bits, b).astype(np.float32))
+    ref = (weff * s.float().repeat_interleave(128, 0)).to(tdt).double().numpy()
+    got = O.graded_weight_rounded(W, bits, s.double().numpy(), b, 128, dtype)
+    assert np.array_equal(got, ref)
+    all_bits = O.grade(x, [-1.0] * 4, b)
+    assert np.array_equal(O.graded_weight_rounded(W, all_bits, s.double().numpy(), b, 128, dtype),
+                          O.dense_weight(W, s.double().numpy(), 128, dtype))
+
+
+def test_rounded_union_product_and_dense_exact():
+    """The rounded S10 product is x @ RNE(w_eff*s); the exact dense product is
+    the all-zones S10 (tests/test_grinqh_ops.py:170, 190); with every zone
+    active the rounded S10 is S9 (grinqh/kernel.py:586-587)."""
+    rng = np.random.default_rng(14)
+    W = _rand_w(rng, 256, 64, 8)
+    x = rng.standard_normal((3, 256)).astype(np.float16)
+    s = rng.standard_normal((2, 64)).astype(np.float16)
+    np.testing.assert_allclose(O.dense_exact_f64(x, W, s, 128), O.gemv_union_f64(x, W, s, [-1.0] * 4, 8, 128),
+                               rtol=1e-12, atol=1e-9)
+    np.testing.assert_array_equal(O.gemv_union_rounded_f64(x, W, s, [-1.0] * 4, 8, 128, "float16"),
+                                  O.dense_prefill_f64(x, W, s, 128, "float16"))
+    t = [0.0, 0.5, 1.0, 2.0]
+    sigma = np.abs(x.astype(np.float32)).max(0)
+    wr = O.graded_weight_rounded(W, O.grade(sigma, t, 8), s, 8, 128, "float16")
+    np.testing.assert_array_equal(O.gemv_union_rounded_f64(x, W, s, t, 8, 128, "float16"),
+                                  x.astype(np.float64) @ wr)
+
+
+@pytest.mark.parametrize("b", [4, 8])
+def test_cpu_reference_matches_oracle(b):
+    """The CPU baseline (oracle/cpu_reference.py, torch eager) computes what
+    the oracle does: the same int8 weights from the planes, S10 graded math and
+    S9 dense math on the same inputs."""
+    from oracle import cpu_reference as C
+    rng = np.random.default_rng(15 + b)
+    K, N, M = 256, 192, 5
+    W = _rand_w(rng, K, N, b)
+    P = torch.from_numpy(O.prepare_weight(W, b).view(np.int32))
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    s = (rng.standard_normal((K // 128, N)) * 0.05).astype(np.float16)
+    assert np.array_equal(C.weight_int8(P, b).numpy(), W)
+    t = [0.0] + np.quantile(np.abs(x).astype(np.float32).max(0), [0.5, 0.8, 0.95]).tolist()
+    yg = C.graded(torch.from_numpy(x), P, torch.from_numpy(s), t, 128, b).double().numpy()
+    ref = O.gemv_union(x, W, s, None, t, b, 128, "float16")
+    np.testing.assert_allclose(yg, ref, rtol=2e-3, atol=2e-3 * np.sqrt(np.mean(ref ** 2)))
+    yd = C.dense_prefill(torch.from_numpy(x), P, torch.from_numpy(s), 128, b).double().numpy()
+    refd = O.dense_prefill(x, W, s, None, 128, "float16")
+    np.testing.assert_allclose(yd, refd, rtol=2e-3, atol=2e-3 * np.sqrt(np.mean(refd ** 2)))

@@ -113,8 +113,17 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
   if (!aligned(y, 8) || !aligned(scale, 2)) return GRINQH_ERR_INVALID;
   // plane words are addressed with 32-bit byte offsets (bit 31 reserved)
   if (K * (max_bits / 2) * (N / 16) * 4 >= ((int64_t)1 << 31)) return GRINQH_ERR_INVALID;
+  // the GEMV / decode kernels address the x rows of one launch (at most
+  // kDecodeMaxRows) through 32-bit buffer offsets as well
+  const int64_t rows_per_launch = M < kDecodeMaxRows ? M : kDecodeMaxRows;
+  if (rows_per_launch * ldx * 2 >= ((int64_t)1 << 31)) return GRINQH_ERR_INVALID;
   return GRINQH_OK;
 }
+
+// The fused prefill kernel addresses all of x through one 32-bit buffer
+// descriptor; only the library-GEMM path (64-bit addressing throughout) takes
+// larger activations.
+bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64_t)1 << 31); }
 
 // M > kDecodeMaxRows: the library-GEMM path (use_library_gemm), else one fused
 // prefill launch over the whole batch (graded batches
@@ -143,6 +152,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     }
     return rc;
   }
+  if (!x_fits_fused_prefill(M, d.ldx)) return GRINQH_ERR_INVALID;  // x of 2 GiB or more: split the batch
   PrefillParams p{};
   p.x = xs;
   p.ldx = d.ldx;

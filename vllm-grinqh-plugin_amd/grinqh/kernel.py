@@ -44,10 +44,18 @@ class _Workspaces:
 
     Grown on demand and zero-filled when allocated (the library keeps its
     counters zero between calls).  Calls on one stream are ordered, so they
-    may share it; different streams get different buffers."""
+    may share it; different streams get different buffers.
+
+    A buffer that is outgrown is retired, never freed: a HIP graph captured
+    while it was current keeps its address and writes into it on every
+    replay, so returning it to the allocator would let those replays
+    overwrite whatever tensor is placed there next.  A retired buffer's
+    counters are still zero (every call leaves them so), so such a replay
+    stays correct."""
 
     def __init__(self):
         self._bufs = {}
+        self._retired = []
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
@@ -62,9 +70,16 @@ class _Workspaces:
                         "GRINQH: workspace must be allocated before graph capture; run the largest "
                         "batch once eagerly first")
                 size = max(nbytes, 1 << 20)
+                if buf is not None:
+                    self._retired.append(buf)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
+
+    def retired_bytes(self) -> int:
+        """Bytes held by outgrown workspaces (kept alive for captured graphs)."""
+        with self._lock:
+            return sum(b.numel() for b in self._retired)
 
 
 _WORKSPACES = _Workspaces()
