@@ -180,14 +180,14 @@ __device__ __forceinline__ int midpoint_bias(uint32_t bits) {
 
 // ---------------------------------------------------------------- unpack
 
-// Bit-field insert (v_bfi_b32): bits of `a` where `m` is set, bits of `b` elsewhere.
-// Written as one instruction: left to itself the compiler splits chains of
-// these with constant masks into and/or sequences of twice the length.
-__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
-  return r;
-}
+// Bit-field insert: bits of `a` where `m` is set, bits of `b` elsewhere, in the
+// bit-select form the backend turns into v_bfi_b32 where it can.  It must stay
+// ordinary code: the compiler inserts the wait states an MFMA's result write
+// needs before a later VALU write of the same register only for instructions
+// it can see.  As inline asm this was not done, and a v_bfi_b32 that reused a
+// register of an in-flight MFMA's unused result elements (the one-row GEMV's
+// accumulators have three) was overwritten when the MFMA's write landed last.
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return ((a ^ b) & m) ^ b; }
 
 // Code-byte rebuild for 8 rows of plane words D[e][z] (one word per plane).
 // Plane z's digit of slot j sits in field 3-j of each byte (bits 8*beta+6-2j).
