@@ -302,10 +302,12 @@ def main() -> int:
         log("pmc pass: calibration kernel (torch.neg, 256 MiB in, 256 MiB out) done")
         return 0
 
-    # per-case product time: one graph of enough launches (cycling the shape's
-    # pool) that a copy is re-read only after >= 1 GiB of weight traffic
+    # per-case product time: one graph with one launch per copy of the shape's
+    # pool, so that every replay reads each copy once and a copy is re-read
+    # only after the rest of the pool (>= 2 GiB of copies) has been read
+    rot.min_gap = None
     for c in cases:
-        reps = max(args.reps, math.ceil((1 << 30) / c["touched"]))
+        reps = len(pools[c["shape"]])
         g = torch.cuda.CUDAGraph()
         rot.record()
         with torch.cuda.stream(stream):
@@ -405,9 +407,11 @@ def main() -> int:
         del k["us"], k["bytes"]
 
     def prefill_time_us(name, K, N, M, x, t, mode, n_it):
-        """Graph-timed product on rotated copies (every plane fetched counts as touched)."""
+        """Graph-timed product on rotated copies (every plane fetched counts as
+        touched); at least n_it launches and at most one per copy of the pool,
+        so that a replay reads each copy once."""
         touched = K * N * BITS // 8 + (K // GS) * N * 2
-        n_it = max(n_it, math.ceil((1 << 30) / touched))  # a copy re-read after >= 1 GiB
+        n_it = min(len(pools[name]), max(n_it, math.ceil((1 << 30) / touched)))
         rot.record()
         us = graph_time_us(torch, stream, lambda j: run_product(
             x, *rot.take(name, touched), None, BITS, GS, N // 4, t, mode), n_it)
@@ -415,6 +419,7 @@ def main() -> int:
         return us
 
     # ---------------- prefill at M=2048 (dense dequantize-then-matmul, reference dispatch for M>1)
+    rot.min_gap = None
     prefill = None
     if not args.no_prefill:
         prefill = []
@@ -460,7 +465,7 @@ def main() -> int:
             for M in M_70B:
                 x = synth_x(torch, M, K, 299 + i, dev)
                 t = [-1.0] * 4
-                n_it = max(4, math.ceil((1 << 30) / touched))  # a copy re-read after >= 1 GiB
+                n_it = min(len(brot.pools[name]), max(4, math.ceil((1 << 30) / touched)))
                 with torch.cuda.stream(stream):
                     for _ in range(2):
                         run_product(x, *brot.take(name, touched), None, BITS, GS, N // 4, t, "union")
