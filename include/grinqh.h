@@ -31,6 +31,10 @@ extern "C" {
 #define GRINQH_ERR_INVALID 1     /* bad shape / dtype / bit width / alignment: ValueError in Python */
 #define GRINQH_ERR_HIP 2         /* HIP launch error: RuntimeError in Python */
 #define GRINQH_ERR_WORKSPACE 3   /* workspace missing or smaller than grinqh_workspace_bytes() */
+#define GRINQH_ERR_SCRATCH 4     /* grinqh_gemm_or_gemv_noalloc: the product needs more scratch than it holds */
+
+/* Device scratch held by the allocation-free entry point on every GPU it runs on. */
+#define GRINQH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 
 /* activation / scale / output dtype */
 #define GRINQH_DTYPE_F16 0
@@ -121,6 +125,25 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
                          const void* planes_u32, const void* scale, const void* bias, void* y,
                          int max_bits, int group_size, void* workspace, size_t workspace_bytes,
                          void* stream);
+
+/* Allocation-free quantized linear.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, semantics and results as grinqh_gemm_or_gemv, without the
+ * workspace: its split-K counters, partial sums and grading statistic live in
+ * a fixed device array of GRINQH_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU
+ * holds from the first call until the process ends.  It calls no allocator.
+ * Every batch size runs on the fused kernels (the library-GEMM prefill path,
+ * which needs a 2*N*K dense weight buffer, is not taken), and a product whose
+ * scratch would exceed the array returns GRINQH_ERR_SCRATCH.  All calls on one
+ * GPU share the array, so calls that overlap in time on one GPU (different
+ * streams, or several threads) race; calls ordered on one stream do not.
+ * The device current in the calling thread must be the one that holds the
+ * pointers and the stream. */
+int grinqh_gemm_or_gemv_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                                const void* planes_u32, const void* scale, const void* bias, void* y,
+                                int max_bits, int group_size, const float thresholds[4], int mode,
+                                void* stream);
 
 /* Benchmark instrumentation; no counterpart in the reference.  Arms a one-shot
  * timer: in the next grinqh_gemm_or_gemv / grinqh_gemv_batch_union /

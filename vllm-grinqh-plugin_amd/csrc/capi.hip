@@ -9,6 +9,9 @@
 
 using namespace grinqh;
 
+// Scratch of the allocation-free entry point (see scratch_on_current_device).
+static __device__ __align__(256) unsigned char scratch[GRINQH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr int kAbiVersion = 1;
@@ -74,7 +77,7 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 // depend on the dtype: when either dtype may take the library path (bf16
 // from fewer rows) its regions follow those of the fused kernel, so either
 // path runs from the same workspace.
-WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
+WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow_library = true) {
   WorkspaceLayout w{};
   size_t partial = 0;
   if (M <= kDecodeMaxRows) {
@@ -90,8 +93,8 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode) {
   w.sigma_off = kCounterBytes;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
-  w.library_gemm = M > kDecodeMaxRows && (use_library_gemm(M, N, GRINQH_DTYPE_F16) ||
-                                          use_library_gemm(M, N, GRINQH_DTYPE_BF16));
+  w.library_gemm = allow_library && M > kDecodeMaxRows &&
+                   (use_library_gemm(M, N, GRINQH_DTYPE_F16) || use_library_gemm(M, N, GRINQH_DTYPE_BF16));
   if (w.library_gemm) {
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.chunk_off = round_up(w.partial_off + partial, 256);
@@ -190,9 +193,14 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   return rc;
 }
 
+// allow_library = false keeps every batch on the fused kernels (no dense
+// weight buffer), and a workspace too small for the product's layout is
+// reported as GRINQH_ERR_SCRATCH instead of GRINQH_ERR_WORKSPACE (the
+// allocation-free entry point's fixed scratch).
 int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, const void* planes,
                 const void* scale, const void* bias, void* y, int max_bits, int group_size,
-                const float* thresholds, int mode, void* workspace, size_t ws_bytes, void* stream) {
+                const float* thresholds, int mode, void* workspace, size_t ws_bytes, void* stream,
+                bool allow_library = true) {
   int rc = check_product_args(x, M, K, ldx, N, dtype, planes, scale, y, max_bits, group_size);
   if (rc != GRINQH_OK) return rc;
   if (mode != GRINQH_MODE_REFERENCE && mode != GRINQH_MODE_UNION && mode != GRINQH_MODE_DENSE)
@@ -201,9 +209,9 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
   if (graded && thresholds == nullptr) return GRINQH_ERR_INVALID;
 
-  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE);
+  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE, allow_library);
   if (wl.total > 0 && (workspace == nullptr || ws_bytes < wl.total || !aligned(workspace, 256)))
-    return GRINQH_ERR_WORKSPACE;
+    return allow_library ? GRINQH_ERR_WORKSPACE : GRINQH_ERR_SCRATCH;
   hipStream_t st = as_stream(stream);
   char* ws = static_cast<char*>(workspace);
 
@@ -252,6 +260,54 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   return GRINQH_OK;
 }
 
+// ---- allocation-free entry point (grinqh_gemm_or_gemv_noalloc)
+//
+// Its split-K counters, partial sums and grading statistic live in this
+// file-scope device array; every GPU the library runs on holds its own copy
+// until the process ends.  In host code `scratch` names a host-side stand-in,
+// never device memory: its device address is looked up once per device with
+// hipGetSymbolAddress (that device current) and only that address is used.
+constexpr size_t kScratchBytes = GRINQH_NOALLOC_SCRATCH_BYTES;
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  void* ptr = nullptr;   // device address of `scratch` on this device
+  bool cleared = false;  // counter area cleared on a stream once
+};
+std::mutex g_scratch_mu;
+ScratchSlot g_scratch[kMaxDevices];
+
+__global__ void clear_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The scratch address on the current device.  The first call on a device
+// also clears the split-K counter area with a fill kernel on `st` (device
+// globals start zeroed; this makes it so whatever the loader did), which a
+// graph under capture may record: it only ever writes zeros where every
+// call leaves zeros.
+int scratch_on_current_device(void** out, hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GRINQH_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot& slot = g_scratch[dev];
+  if (slot.ptr == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return GRINQH_ERR_HIP;
+    slot.ptr = p;
+  }
+  if (!slot.cleared) {
+    constexpr int words = (int)(kCounterBytes / 4);
+    hipLaunchKernelGGL(clear_words_kernel, dim3((words + 255) / 256), dim3(256), 0, st,
+                       static_cast<uint32_t*>(slot.ptr), words);
+    if (hipGetLastError() != hipSuccess) return GRINQH_ERR_HIP;
+    slot.cleared = true;
+  }
+  *out = slot.ptr;
+  return GRINQH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -264,6 +320,8 @@ const char* grinqh_status_string(int status) {
     case GRINQH_ERR_INVALID: return "invalid argument (shape, dtype, bit width, alignment or mode)";
     case GRINQH_ERR_HIP: return "HIP kernel launch failed";
     case GRINQH_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
+    case GRINQH_ERR_SCRATCH:
+      return "problem needs more scratch than the allocation-free entry point holds (GRINQH_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
@@ -349,6 +407,19 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
                          int group_size, void* workspace, size_t workspace_bytes, void* stream) {
   return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, nullptr,
                      GRINQH_MODE_DENSE, workspace, workspace_bytes, stream);
+}
+
+int grinqh_gemm_or_gemv_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                                const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
+                                int group_size, const float thresholds[4], int mode, void* stream) {
+  // arguments first: an invalid call touches no device state
+  int rc = check_product_args(x, M, K, ldx, N, dtype, planes_u32, scale, y, max_bits, group_size);
+  if (rc != GRINQH_OK || M == 0) return rc;
+  void* ws = nullptr;
+  rc = scratch_on_current_device(&ws, as_stream(stream));
+  if (rc != GRINQH_OK) return rc;
+  return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds, mode, ws,
+                     kScratchBytes, stream, /*allow_library=*/false);
 }
 
 int grinqh_time_next_product(void* event_before, void* event_after) {

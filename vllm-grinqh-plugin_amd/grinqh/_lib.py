@@ -16,6 +16,8 @@ GRINQH_OK = 0
 GRINQH_ERR_INVALID = 1
 GRINQH_ERR_HIP = 2
 GRINQH_ERR_WORKSPACE = 3
+GRINQH_ERR_SCRATCH = 4
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -47,6 +49,8 @@ SIGNATURES = {
                                        _vp, ctypes.c_size_t, _vp]),
     "grinqh_prefill_dense": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32,
                                     _vp, ctypes.c_size_t, _vp]),
+    "grinqh_gemm_or_gemv_noalloc": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32,
+                                           _f4, _i32, _vp]),
     "grinqh_time_next_product": (_i32, [_vp, _vp]),
 }
 
@@ -89,7 +93,7 @@ def check(status: int, what: str) -> None:
     if status == GRINQH_OK:
         return
     msg = f"{what}: {load_library().grinqh_status_string(status).decode()} (status {status})"
-    if status in (GRINQH_ERR_INVALID, GRINQH_ERR_WORKSPACE):
+    if status in (GRINQH_ERR_INVALID, GRINQH_ERR_WORKSPACE, GRINQH_ERR_SCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)
 
