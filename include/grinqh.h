@@ -126,6 +126,39 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
                          int max_bits, int group_size, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* ---- Producer fusion: the operations that feed a GRINQH linear also emit
+ * the union statistic sigma_k = max_m |y[m][k]| its grading needs
+ * (grinqh/kernel.py:249), as column maxima of row chunks: sigma_chunks is
+ * float [ceil(M / GRINQH_SIGMA_CHUNK_ROWS)][K], the maximum over its chunks is
+ * sigma_k (NaN ignored unless every value is NaN).  No counterpart in the
+ * reference, whose grading reads x again inside the GEMV. */
+#define GRINQH_SIGMA_CHUNK_ROWS 16
+
+/* y = RNE(h * rsqrt(mean_k(h^2) + eps)) * weight with h = x, or, when residual
+ * is given, h = RNE(x + residual) written to residual_out (vLLM's
+ * fused_add_rms_norm arithmetic).  x [M][ldx], residual / residual_out / y
+ * [M][K] dense, weight [K]; all 16-byte aligned, K % 8 == 0.  y must not
+ * overlap x or residual, nor residual_out residual. */
+int grinqh_rmsnorm_sigma(const void* x, int64_t M, int64_t K, int64_t ldx, const void* residual, void* residual_out,
+                         const void* weight, float eps, void* y, float* sigma_chunks, int dtype, void* stream);
+
+/* y[m][f] = RNE(silu(g)) * u with gate_up rows [g (F values) | u (F values)]
+ * ld elements apart (vLLM's SiluAndMul arithmetic); y [M][F] dense, must not
+ * overlap gate_up; F % 8 == 0, 16-byte aligned. */
+int grinqh_silu_mul_sigma(const void* gate_up, int64_t M, int64_t F, int64_t ld, void* y, float* sigma_chunks,
+                          int dtype, void* stream);
+
+/* grinqh_gemv_batch_union grading from the sigma_chunks a producer wrote for
+ * this x (ceil(M / GRINQH_SIGMA_CHUNK_ROWS) arrays of K floats) instead of
+ * reading x for it: batches of 17-64 rows skip the statistic pass.  Larger
+ * batches (prefill) compute their own statistic and ignore sigma_chunks.
+ * Same workspace as grinqh_gemm_or_gemv in GRINQH_MODE_UNION. */
+int grinqh_gemv_batch_union_sigma(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                                  const void* planes_u32, const void* scale, const void* bias, void* y,
+                                  int max_bits, int group_size, const float thresholds[4],
+                                  const float* sigma_chunks, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* Allocation-free quantized linear.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same

@@ -200,7 +200,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
 int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, const void* planes,
                 const void* scale, const void* bias, void* y, int max_bits, int group_size,
                 const float* thresholds, int mode, void* workspace, size_t ws_bytes, void* stream,
-                bool allow_library = true) {
+                bool allow_library = true, const float* sigma_given = nullptr) {
   int rc = check_product_args(x, M, K, ldx, N, dtype, planes, scale, y, max_bits, group_size);
   if (rc != GRINQH_OK) return rc;
   if (mode != GRINQH_MODE_REFERENCE && mode != GRINQH_MODE_UNION && mode != GRINQH_MODE_DENSE)
@@ -231,11 +231,15 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   const uint16_t* xs = static_cast<const uint16_t*>(x);
   uint16_t* ys = static_cast<uint16_t*>(y);
   if (M > kDecodeMaxRows) return run_prefill(p, xs, ys, M, dtype, max_bits, graded, ws, wl, st);
-  if (graded && M > kSigmaPrepassRows) {  // decode above 16 rows grades from the batch statistic
+  if (graded && sigma_given != nullptr) {  // the producer's chunk maxima (grinqh_*_sigma)
+    p.sigma = sigma_given;
+    p.sigma_chunks = (int)((M + kSigmaChunkRows - 1) / kSigmaChunkRows);
+  } else if (graded && M > kSigmaPrepassRows) {  // decode above 16 rows grades from the batch statistic
     float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
     rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sigma, st);
     if (rc != GRINQH_OK) return rc;
     p.sigma = sigma;
+    p.sigma_chunks = 1;
   }
   for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
@@ -420,6 +424,42 @@ int grinqh_gemm_or_gemv_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx
   if (rc != GRINQH_OK) return rc;
   return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds, mode, ws,
                      kScratchBytes, stream, /*allow_library=*/false);
+}
+
+int grinqh_rmsnorm_sigma(const void* x, int64_t M, int64_t K, int64_t ldx, const void* residual, void* residual_out,
+                         const void* weight, float eps, void* y, float* sigma_chunks, int dtype, void* stream) {
+  if (!valid_dtype(dtype) || M < 0 || K <= 0 || K % 8 != 0 || ldx < K || ldx % 8 != 0) return GRINQH_ERR_INVALID;
+  if (K > ((int64_t)1 << 30) || M > ((int64_t)1 << 30) || !(eps >= 0.f)) return GRINQH_ERR_INVALID;
+  if (M == 0) return GRINQH_OK;
+  if (x == nullptr || weight == nullptr || y == nullptr || sigma_chunks == nullptr) return GRINQH_ERR_INVALID;
+  if ((residual == nullptr) != (residual_out == nullptr)) return GRINQH_ERR_INVALID;
+  if (!aligned(x, 16) || !aligned(weight, 16) || !aligned(y, 16) || !aligned(sigma_chunks, 4)) return GRINQH_ERR_INVALID;
+  if (residual != nullptr && (!aligned(residual, 16) || !aligned(residual_out, 16) || residual_out == residual))
+    return GRINQH_ERR_INVALID;
+  if (y == x || y == residual) return GRINQH_ERR_INVALID;  // every block reads whole rows of both
+  return launch_rmsnorm_sigma(static_cast<const uint16_t*>(x), ldx, static_cast<const uint16_t*>(residual),
+                              static_cast<uint16_t*>(residual_out), static_cast<const uint16_t*>(weight), eps,
+                              static_cast<uint16_t*>(y), sigma_chunks, (int)M, (int)K, dtype, as_stream(stream));
+}
+
+int grinqh_silu_mul_sigma(const void* gate_up, int64_t M, int64_t F, int64_t ld, void* y, float* sigma_chunks,
+                          int dtype, void* stream) {
+  if (!valid_dtype(dtype) || M < 0 || F <= 0 || F % 8 != 0 || ld < 2 * F || ld % 8 != 0) return GRINQH_ERR_INVALID;
+  if (F > ((int64_t)1 << 30) || M > ((int64_t)1 << 30)) return GRINQH_ERR_INVALID;
+  if (M == 0) return GRINQH_OK;
+  if (gate_up == nullptr || y == nullptr || sigma_chunks == nullptr) return GRINQH_ERR_INVALID;
+  if (!aligned(gate_up, 16) || !aligned(y, 16) || !aligned(sigma_chunks, 4) || y == gate_up) return GRINQH_ERR_INVALID;
+  return launch_silu_mul_sigma(static_cast<const uint16_t*>(gate_up), ld, static_cast<uint16_t*>(y), sigma_chunks,
+                               (int)M, (int)F, dtype, as_stream(stream));
+}
+
+int grinqh_gemv_batch_union_sigma(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
+                                  const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
+                                  int group_size, const float thresholds[4], const float* sigma_chunks,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (sigma_chunks == nullptr || !aligned(sigma_chunks, 4)) return GRINQH_ERR_INVALID;
+  return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds,
+                     GRINQH_MODE_UNION, workspace, workspace_bytes, stream, /*allow_library=*/true, sigma_chunks);
 }
 
 int grinqh_time_next_product(void* event_before, void* event_after) {

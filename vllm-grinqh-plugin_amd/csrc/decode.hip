@@ -190,7 +190,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     } else {
       float s;
       if (AG || p.sigma != nullptr) {  // batch statistic computed beforehand (always above 16 rows)
-        s = p.sigma[row0 + rr];
+        s = precomputed_sigma(p, row0 + rr);
       } else {
         s = fabsf(to_f32<DT>(s_x[rr]));
         for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));

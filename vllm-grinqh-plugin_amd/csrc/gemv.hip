@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     } else {
       float s;
       if (p.sigma != nullptr) {  // statistic of a whole batch split into several launches
-        s = p.sigma[row0 + rr];
+        s = precomputed_sigma(p, row0 + rr);
       } else {
         s = fabsf(to_f32<DT>(s_x[rr]));
         for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));

@@ -28,7 +28,9 @@ struct DecodeParams {
   int splits;           // grid.y: K ranges
   int tiles_per_split;  // 32-row tiles per K range
   float* partial;       // [splits][M][N] fp32 when splits > 1
-  const float* sigma;   // optional precomputed union statistic [K] (else computed from x)
+  const float* sigma;   // optional precomputed union statistic (else computed from x):
+                        // sigma_chunks arrays of K column maxima whose maximum is sigma_k
+  int sigma_chunks;     // arrays at sigma (1 for a plain [K] statistic)
   uint32_t* counters;   // per column block, zero on entry: the kernel completes split-K
                         // itself; nullptr: partial sums only, the reduce kernel follows
 };
@@ -169,6 +171,22 @@ inline void launch_main_kernel(void (*kernel)(P), dim3 grid, dim3 block, hipStre
   } else {
     hipLaunchKernelGGL(kernel, grid, block, 0, st, p);
   }
+}
+
+// Producer fusion (producer.hip): rows per chunk of the column maxima the
+// producers write, and the producers themselves.
+constexpr int kSigmaChunkRows = 16;
+int launch_rmsnorm_sigma(const uint16_t* x, int64_t ldx, const uint16_t* residual, uint16_t* residual_out,
+                         const uint16_t* weight, float eps, uint16_t* y, float* sigma_chunks, int M, int K, int dtype,
+                         hipStream_t st);
+int launch_silu_mul_sigma(const uint16_t* gu, int64_t ld, uint16_t* y, float* sigma_chunks, int M, int F, int dtype,
+                          hipStream_t st);
+
+// sigma_k of a precomputed statistic: the maximum of its chunk maxima
+__device__ __forceinline__ float precomputed_sigma(const DecodeParams& p, int k) {
+  float s = p.sigma[k];
+  for (int c = 1; c < p.sigma_chunks; ++c) s = fmaxf(s, p.sigma[(int64_t)c * p.K + k]);
+  return s;
 }
 
 int launch_pack_planes(const uint32_t* U, uint32_t* out, int K, int N, int max_bits, hipStream_t st);

@@ -18,6 +18,7 @@ GRINQH_ERR_HIP = 2
 GRINQH_ERR_WORKSPACE = 3
 GRINQH_ERR_SCRATCH = 4
 NOALLOC_SCRATCH_BYTES = 64 << 20
+SIGMA_CHUNK_ROWS = 16
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -51,6 +52,10 @@ SIGNATURES = {
                                     _vp, ctypes.c_size_t, _vp]),
     "grinqh_gemm_or_gemv_noalloc": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32,
                                            _f4, _i32, _vp]),
+    "grinqh_rmsnorm_sigma": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i32, _vp]),
+    "grinqh_silu_mul_sigma": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
+    "grinqh_gemv_batch_union_sigma": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f4,
+                                             _vp, _vp, ctypes.c_size_t, _vp]),
     "grinqh_time_next_product": (_i32, [_vp, _vp]),
 }
 
