@@ -8,7 +8,7 @@ M in {1, 4, 16, 64}; fp16 activations N(0,1) with 1 % of channels x20; weights
 union grading with thresholds [0, P50, P80, P95] of sigma_k = max_m |x[m,k]|.
 One step = the 16 products once.
 
-HBM-cold timing: every shape has a pool of weight copies of at least 2 GiB,
+HBM-cold timing: every shape has a pool of weight copies of at least 3 GiB,
 handed out least recently used first, so that no timed product reads a weight
 copy that was read less than ~0.9 GB of weight traffic earlier (the MI355X
 MALL holds 256 MB).  The smallest distance actually seen between two reads
@@ -52,7 +52,7 @@ M_70B = (1, 64, 4096)
 GS = 128
 BITS = 8
 MALL_BYTES = 256 << 20
-POOL_BYTES = 2 << 30  # weight copies per shape: at least this many bytes
+POOL_BYTES = 3 << 30  # weight copies per shape: at least this many bytes
 
 
 def log(msg: str) -> None:
@@ -195,6 +195,151 @@ def traffic_for(kernel: str):
     return None
 
 
+def llama8b_decode_step(torch, dev, stream, batch: int = 32, layers: int = 32, replays: int = 5):
+    """One-GPU stand-in for BASELINE configs[3] (not the vLLM end-to-end run):
+    the 128 GRINQH linears of a Llama-3-8B decode step at ``batch`` tokens --
+    per layer qkv_proj 4096->6144, o_proj 4096->4096, gate_up_proj
+    4096->28672 and down_proj 14336->4096, every layer with weights of its own
+    (7 GB of planes, so every read comes from HBM) -- through
+    torch.ops.grinqh.gemm_or_gemv, with the glue that feeds them (RMSNorm,
+    residual adds, SiLU(gate)*up; attention is replaced by the query part of
+    the qkv output) in torch.  Per-layer thresholds are calibrated on the
+    step's own activations (P50/P80/P95 of each layer's statistic, zone 0 at
+    0.0) with grinqh.thresholds.  The whole step is captured in one HIP graph
+    per grading mode; the 128 linears alone, on the inputs the step produces,
+    in another."""
+    from grinqh import kernel as gk
+    from grinqh.producer import gemv_batch_union_sigma, rmsnorm_sigma, silu_mul_sigma
+    from grinqh.thresholds import StatsRecorder, llama_prefixes, thresholds_from_statistics
+    from grinqh.utils import grade, prepare_weight
+    H, F = 4096, 14336
+    shapes = {"self_attn.qkv_proj": (H, 6144), "self_attn.o_proj": (H, H), "mlp.gate_up_proj": (H, 2 * F),
+              "mlp.down_proj": (F, H)}
+    prefixes = llama_prefixes(layers)
+    W = {}
+    for i, pfx in enumerate(prefixes):
+        K, N = shapes[pfx.split(".", 3)[3]]
+        w, s = synth_weight(torch, K, N, 5000 + i, dev)
+        W[pfx] = (prepare_weight(w, BITS), s, K, N)
+        del w
+    norm_w = torch.ones(H, device=dev, dtype=torch.float16)
+
+    def rmsnorm(h):
+        hf = h.float()
+        return (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5)).half() * norm_w
+
+    thr = {pfx: [-1.0] * 4 for pfx in prefixes}
+    inputs = {}
+
+    def linear(pfx, x):
+        P, s, K, N = W[pfx]
+        inputs[pfx] = x
+        return torch.ops.grinqh.gemm_or_gemv(x, P, s, None, BITS, GS, N // 4, thr[pfx])
+
+    def step(h):
+        for li in range(layers):
+            base = f"model.layers.{li}."
+            qkv = linear(base + "self_attn.qkv_proj", rmsnorm(h))
+            h = h + linear(base + "self_attn.o_proj", qkv[:, :H].contiguous())
+            gu = linear(base + "mlp.gate_up_proj", rmsnorm(h))
+            h = h + linear(base + "mlp.down_proj", (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).half())
+        return h
+
+    def linear_sig(pfx, x, sig):
+        P, s, K, N = W[pfx]
+        inputs[pfx] = x
+        return gemv_batch_union_sigma(x, P, s, None, BITS, GS, N // 4, thr[pfx], sig)
+
+    def step_fused(h):
+        """Union grading with producer fusion: the RMSNorms (residual add
+        included) and SiLU*mul emit the statistic their consumer grades on."""
+        hn, sig, _ = rmsnorm_sigma(h, norm_w)
+        res = h
+        for li in range(layers):
+            base = f"model.layers.{li}."
+            qkv = linear_sig(base + "self_attn.qkv_proj", hn, sig)
+            o = linear(base + "self_attn.o_proj", qkv[:, :H].contiguous())
+            hn, sig, res = rmsnorm_sigma(o, norm_w, 1e-5, res)
+            gu = linear_sig(base + "mlp.gate_up_proj", hn, sig)
+            a, asig = silu_mul_sigma(gu)
+            d = linear_sig(base + "mlp.down_proj", a, asig)
+            hn, sig, res = rmsnorm_sigma(d, norm_w, 1e-5, res)
+        return res
+
+    h0 = synth_x(torch, batch, H, 77, dev) * 0.05
+    out = {"batch": batch, "layers": layers, "linears": len(prefixes),
+           "note": "stand-in for BASELINE configs[3]: the quantized linears of a Llama-3-8B decode step on one "
+                   "GPU with torch glue and no attention; the vLLM end-to-end run was not done"}
+    saved = gk.batch_grading_mode()
+    try:
+        gk.set_batch_grading_mode("reference")
+        with torch.cuda.stream(stream):
+            step(h0)  # calibration pass (dense, reference dispatch)
+            torch.cuda.synchronize()
+        rec = StatsRecorder()
+        for pfx in prefixes:
+            rec.update(pfx, inputs[pfx])
+        calibrated = thresholds_from_statistics({p: rec.samples(p) for p in prefixes})
+        for mode in ("reference", "union", "union_fused"):
+            gk.set_batch_grading_mode("reference" if mode == "reference" else "union")
+            thr.update(calibrated)
+            fn = step_fused if mode == "union_fused" else step
+            with torch.cuda.stream(stream):
+                fn(h0)
+                torch.cuda.synchronize()
+                g_step = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g_step, stream=stream):
+                    fn(h0)
+                g_step.replay()  # fills the captured step's tensors, the linears' inputs among them
+                torch.cuda.synchronize()
+                xs = {p: inputs[p].clone() for p in prefixes}
+                sigs = {}
+                if mode == "union_fused":  # each graded input's chunk maxima, as its producer gives them
+                    for p in prefixes:
+                        if not p.endswith("o_proj"):
+                            xv = xs[p].float().abs()
+                            sigs[p] = torch.stack([xv[c:c + 16].amax(0) for c in range(0, batch, 16)])
+                g_lin = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g_lin, stream=stream):
+                    for p in prefixes:  # the linears alone (union_fused: each with its statistic given)
+                        P, s, K, N = W[p]
+                        if mode == "union_fused" and p in sigs:
+                            gemv_batch_union_sigma(xs[p], P, s, None, BITS, GS, N // 4, thr[p], sigs[p])
+                        else:
+                            torch.ops.grinqh.gemm_or_gemv(xs[p], P, s, None, BITS, GS, N // 4, thr[p])
+                times = {}
+                for name, g in (("step", g_step), ("linears", g_lin)):
+                    g.replay()
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    for _ in range(replays):
+                        g.replay()
+                    e1.record(stream)
+                    e1.synchronize()
+                    times[name] = e0.elapsed_time(e1) * 1e3 / replays
+            nbytes = 0
+            for p in prefixes:
+                P, s, K, N = W[p]
+                if mode != "reference":
+                    zb, _ = grade(xs[p], thr[p], BITS)
+                    planes = int(np.unpackbits(zb.cpu().numpy()[:, None], axis=1).sum()) * (N // 4)
+                else:
+                    planes = K * N * BITS // 8
+                nbytes += planes + (K // GS) * N * 2 + batch * (K + N) * 2
+            out[mode] = {"step_us": round(times["step"], 1), "linears_us": round(times["linears"], 1),
+                         "linear_bytes": nbytes, "linears_gbs": round(nbytes / (times["linears"] * 1e-6) / 1e9, 1),
+                         "frac_of_hbm": round(nbytes / (times["linears"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            log(f"llama-3-8b decode step batch {batch} ({mode}): step {times['step']:.0f} us, 128 linears "
+                f"{times['linears']:.0f} us, {out[mode]['linears_gbs']:.0f} GB/s")
+            del g_step, g_lin, xs
+    finally:
+        gk.set_batch_grading_mode(saved)
+    del W
+    torch.cuda.empty_cache()
+    return out
+
+
 def touched_bytes(rec) -> int:
     """Weight bytes a product reads: the planes its grading needs and the scales."""
     return rec["bytes"] - rec["M"] * rec["K"] * 2 - rec["M"] * rec["N"] * 2
@@ -209,6 +354,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B shape sweep (BASELINE configs[4])")
+    ap.add_argument("--no-model-step", action="store_true",
+                    help="skip the Llama-3-8B decode-step stand-in (BASELINE configs[3])")
     ap.add_argument("--prefill-case", default=None, metavar="SHAPE:M:MODE",
                     help="profiling run: one prefill product (e.g. gate_up:2048:union; MODE dense or union with "
                          "t = [0, P70, P90, P98]) twice as warm-up and twice counted; prints no JSON line")
@@ -500,6 +647,9 @@ def main() -> int:
             del brot, base, s
             torch.cuda.empty_cache()
 
+    # ---------------- BASELINE configs[3] stand-in: the linears of a Llama-3-8B decode step at batch 32
+    model_step = None if args.no_model_step else llama8b_decode_step(torch, dev, stream)
+
     # ---------------- CPU baseline: the reference's pure-PyTorch math on the host cores, over the
     # whole decode sweep (graded union math), plus its dense dispatch (S9) at 16 rows
     cpu = None
@@ -569,6 +719,7 @@ def main() -> int:
         "prefill": prefill,
         "prefill_graded": prefill_graded,
         "llama70b_adversarial": big,
+        "llama8b_decode_step": model_step,
     }
     print(json.dumps(out), flush=True)
     return 0

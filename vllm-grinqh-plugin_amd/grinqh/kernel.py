@@ -39,6 +39,17 @@ def batch_grading_mode() -> str:
     return _BATCH_GRADING
 
 
+def set_batch_grading_mode(mode: str) -> None:
+    """Set the op's batch grading mode ("reference" or "union") for the calls
+    that follow, as GRINQH_BATCH_GRADING does at import.  A HIP graph keeps
+    the mode it was captured with."""
+    global _BATCH_GRADING
+    mode = mode.strip().lower()
+    if mode not in ("reference", "union"):
+        raise ValueError(f"batch grading mode must be 'reference' or 'union', got {mode!r}")
+    _BATCH_GRADING = mode
+
+
 class _Workspaces:
     """Per (device, stream) workspace: split-K counters and partial sums.
 
