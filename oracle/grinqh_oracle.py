@@ -24,6 +24,9 @@ other than itself):
                                       strict ``>``), special cases t=-1 (all zones)
                                       and quantile 1.0 (no zone), brute force over all
                                       fp16 values against a threshold pair.
+* ``union_sigma``                  -- NaN rule of Triton's ``tl.max`` read from the
+                                      installed Triton (3.6.0; the reference pins 3.7.1,
+                                      uv.lock:5094), padding rule brute-forced on tiny batches.
 * ``effective_weight``             -- closed form ``floor(c / 2^(b-2a)) * 2^(b-2a) + 2^(b-2a-1)``
                                       for prefix masks, and the reference test oracle's
                                       dense form (tests/test_grinqh_ops.py:28-55).
@@ -37,7 +40,7 @@ import numpy as np
 
 __all__ = [
     "preshuffle", "postshuffle", "shift_codes", "pack_planes", "unpack_planes",
-    "prepare_weight", "grade", "zone_mask_byte", "midpoint_bias", "effective_weight",
+    "prepare_weight", "grade", "union_sigma", "zone_mask_byte", "midpoint_bias", "effective_weight",
     "masked_weight_ref", "gemv_f64", "gemv", "gemv_union_f64", "gemv_union",
     "dense_prefill", "dense_prefill_f64", "gemm_or_gemv", "to_f32_threshold",
     "rne_cast", "bias_add",
@@ -245,14 +248,31 @@ def gemv(x, w_int8, scale, bias, thresholds, max_bits, group_size, dtype="float1
     return bias_add(gemv_f64(x, w_int8, scale, thresholds, max_bits, group_size), bias, dtype)
 
 
+def union_sigma(x: np.ndarray) -> np.ndarray:
+    """Statistic of the batch-union grading, ``sigma_k = max_m |x[m,k]|``
+    (grinqh/kernel.py:237-249).  The kernel holds the batch in one tile of
+    ``BLOCK_BATCH = next_power_of_2(M)`` rows (:196-197, :632) whose rows past
+    ``M`` load as 0.0 (``other=0.0``, :240-245), and reduces ``|x|`` with
+    ``tl.max``, which combines pairs with ``tl.maximum`` at its default
+    ``propagate_nan=NONE`` -- a NaN-ignoring maximum (maxnum).  So NaN entries
+    are ignored, and a column whose entries are all NaN has statistic NaN
+    when ``M`` is a power of two and 0.0 (the padding rows) otherwise."""
+    x = np.asarray(x, dtype=np.float64)
+    sigma = np.fmax.reduce(np.abs(x), axis=0)
+    M = x.shape[0]
+    if M & (M - 1):
+        sigma = np.fmax(sigma, 0.0)
+    return sigma
+
+
 def gemv_union_f64(x: np.ndarray, w_int8: np.ndarray, scale: np.ndarray, thresholds, max_bits: int,
                    group_size: int) -> np.ndarray:
-    """S10: grade row ``k`` on ``sigma_k = max_m |x[m,k]|`` (grinqh/kernel.py:249-289),
-    then ``y[m,n] = sum_k x[m,k] w_eff[k,n] scale[k//gs,n]`` (:339-344).  NaN
-    entries are ignored by the max."""
+    """S10: grade row ``k`` on ``sigma_k = max_m |x[m,k]|`` (``union_sigma``,
+    grinqh/kernel.py:249-289), then ``y[m,n] = sum_k x[m,k] w_eff[k,n]
+    scale[k//gs,n]`` (:339-344)."""
     x = np.asarray(x, dtype=np.float64)
     K = x.shape[1]
-    sigma = np.fmax.reduce(np.abs(x), axis=0)
+    sigma = union_sigma(x)
     bits = grade(sigma, thresholds, max_bits)
     weff = effective_weight(w_int8, bits, max_bits).astype(np.float64)
     return x @ (weff * _scale_rows(scale, K, group_size))
@@ -291,7 +311,7 @@ def gemv_union_rounded_f64(x: np.ndarray, w_int8: np.ndarray, scale: np.ndarray,
     before the product: ``x @ graded_weight_rounded(...)`` in float64, grading
     on the union statistic (grinqh/kernel.py:249-289)."""
     x = np.asarray(x, dtype=np.float64)
-    sigma = np.fmax.reduce(np.abs(x), axis=0)
+    sigma = union_sigma(x)
     bits = grade(sigma, thresholds, max_bits)
     return x @ graded_weight_rounded(w_int8, bits, scale, max_bits, group_size, dtype)
 

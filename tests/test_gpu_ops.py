@@ -142,10 +142,30 @@ def test_grade_bit_exact(b, dtype):
             xt = _tdt(x, dtype)
             bits, beta = grade(xt, t, b)
             xs = xt.double().cpu().numpy()
-            sigma = np.fmax.reduce(np.abs(xs), axis=0)
-            eb = O.grade(sigma, t, b)
+            eb = O.grade(O.union_sigma(xs), t, b)
             np.testing.assert_array_equal(bits.cpu().numpy(), eb, err_msg=f"t={t} M={M}")
             np.testing.assert_array_equal(beta.cpu().numpy(), O.midpoint_bias(eb, b))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_grade_all_nan_column_follows_batch_padding(dtype):
+    """A column whose entries are all NaN: its statistic is NaN for a batch of
+    a power-of-two size (no zone) and 0.0 otherwise (the padding rows of the
+    reference's batch tile), so negative thresholds turn zones on."""
+    from grinqh.utils import grade
+    rng = np.random.default_rng(41)
+    t = [-1.0, 0.0, -0.5, 1.0]
+    for M in (1, 2, 3, 4, 5, 8, 17, 20, 64, 100):
+        x = to_dtype_np(rng.standard_normal((M, 300)), dtype)
+        x[:, 7] = np.nan
+        x[:, 250] = np.nan
+        x[0, 100] = np.nan
+        xt = _tdt(x, dtype)
+        bits, beta = grade(xt, t, 8)
+        eb = O.grade(O.union_sigma(xt.double().cpu().numpy()), t, 8)
+        assert eb[7] == (0 if M & (M - 1) == 0 else 0b0101), M
+        np.testing.assert_array_equal(bits.cpu().numpy(), eb, err_msg=f"M={M}")
+        np.testing.assert_array_equal(beta.cpu().numpy(), O.midpoint_bias(eb, 8))
 
 
 # ----------------------------------------------------------------------- products

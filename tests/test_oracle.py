@@ -113,6 +113,44 @@ def test_grade_special_cases(b):
     assert np.all(O.grade(x, [q1] * 4, b) == 0)
 
 
+def test_union_sigma_nan_and_padding_rule():
+    """union_sigma against its two sources.  (1) Triton's tl.max: its combine
+    is tl.maximum at the default propagate_nan, which lowers to maxnum (NaN
+    ignored); read from the installed Triton (the reference pins 3.7.1 in
+    uv.lock, absent here).  (2) The batch tile of next_power_of_2(M) rows with
+    zero padding: brute force over tiny batches by an explicit tile."""
+    triton = pytest.importorskip("triton")
+    import inspect
+    from triton.language import core, standard
+    from triton.language.semantic import TritonSemantic
+    assert "core.maximum(a, b)" in inspect.getsource(standard._elementwise_max.fn)
+    assert inspect.signature(core.maximum).parameters["propagate_nan"].default == core.PropagateNan.NONE
+    src = inspect.getsource(TritonSemantic.maximum)
+    assert src.index("PropagateNan.NONE") < src.index("create_maxnumf") < src.index("raise ValueError")
+    assert triton.__version__.startswith("3.")
+
+    def maxnum(a, b):  # IEEE maxNum: a NaN operand loses to a number
+        return b if np.isnan(a) else a if np.isnan(b) else max(a, b)
+
+    rng = np.random.default_rng(3)
+    for M in range(1, 10):
+        for _ in range(20):
+            x = rng.standard_normal((M, 5))
+            x[rng.random((M, 5)) < 0.4] = np.nan
+            x[:, 0] = np.nan  # one column all NaN
+            B = 1 << (M - 1).bit_length()
+            tile = np.zeros((B, 5))
+            tile[:M] = x
+            exp = np.empty(5)
+            for k in range(5):
+                acc = abs(tile[0, k])
+                for m in range(1, B):
+                    acc = maxnum(acc, abs(tile[m, k]))
+                exp[k] = acc
+            np.testing.assert_array_equal(O.union_sigma(x), exp)
+        assert np.isnan(O.union_sigma(np.full((M, 1), np.nan))[0]) == (M & (M - 1) == 0)
+
+
 @pytest.mark.parametrize("b", BITS)
 def test_effective_weight_prefix_closed_form(b):
     """Prefix of `a` active zones keeps the top 2a bits and adds the midpoint of

@@ -111,15 +111,23 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
 
 // Grading export (reference inline grading, grinqh/kernel.py:98-114 for one
 // row and :249-289 for the batch union): per weight row k, the zone bits of
-// sigma_k = max_m |x[m][k]| (NaN ignored unless every entry is NaN) and the
-// midpoint bias beta_k.
+// sigma_k = max_m |x[m][k]| (NaN ignored) and the midpoint bias beta_k.
+//
+// A column whose entries are all NaN: the reference holds the batch in one
+// tile of next_power_of_2(M) rows whose rows past M load as 0.0
+// (grinqh/kernel.py:196-197, 240-245, 632) and reduces with a NaN-ignoring
+// maximum, so the statistic is 0.0 when M is not a power of two (zone z on
+// iff 0 > t_z, the `nan_bits` given here) and NaN, no zone, otherwise.  Only
+// this export can show the difference: in a product every output of such a
+// batch is NaN whatever the grading.
 template <int Z, typename DT>
 __global__ __launch_bounds__(256) void grade_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                    int K, GradeThresholds thr, uint8_t* __restrict__ bits,
-                                                    int32_t* __restrict__ beta) {
+                                                    int K, GradeThresholds thr, uint32_t nan_bits,
+                                                    uint8_t* __restrict__ bits, int32_t* __restrict__ beta) {
   const int k = blockIdx.x * blockDim.x + threadIdx.x;
   if (k >= K) return;
-  const uint32_t b = zone_bits<Z>(column_absmax<DT>(x, ldx, M, k), thr.t);
+  const float s = column_absmax<DT>(x, ldx, M, k);
+  const uint32_t b = s == s ? zone_bits<Z>(s, thr.t) : nan_bits & ((1u << Z) - 1u);
   bits[k] = (uint8_t)b;
   if (beta != nullptr) beta[k] = midpoint_bias<Z>(b);
 }
@@ -181,14 +189,18 @@ int launch_grade(const uint16_t* x, int64_t ldx, int M, int K, const float* t, i
                  uint8_t* bits, int32_t* beta, hipStream_t st) {
   if (K == 0) return GRINQH_OK;
   GradeThresholds thr;
-  for (int i = 0; i < 4; ++i) thr.t[i] = t[i];
+  uint32_t nan_bits = 0;  // zone bits of an all-NaN column: 0 > t_z when M is not a power of two
+  for (int i = 0; i < 4; ++i) {
+    thr.t[i] = t[i];
+    if ((M & (M - 1)) != 0 && 0.f > t[i]) nan_bits |= 1u << i;
+  }
   const dim3 grid(blocks_for(K));
   if (dtype == GRINQH_DTYPE_BF16) {
     GRINQH_SWITCH_Z(max_bits / 2,
-      hipLaunchKernelGGL((grade_kernel<Z_, BF16>), grid, dim3(256), 0, st, x, ldx, M, K, thr, bits, beta));
+      hipLaunchKernelGGL((grade_kernel<Z_, BF16>), grid, dim3(256), 0, st, x, ldx, M, K, thr, nan_bits, bits, beta));
   } else {
     GRINQH_SWITCH_Z(max_bits / 2,
-      hipLaunchKernelGGL((grade_kernel<Z_, F16>), grid, dim3(256), 0, st, x, ldx, M, K, thr, bits, beta));
+      hipLaunchKernelGGL((grade_kernel<Z_, F16>), grid, dim3(256), 0, st, x, ldx, M, K, thr, nan_bits, bits, beta));
   }
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
