@@ -14,7 +14,7 @@ import torch
 
 from oracle import grinqh_oracle as O
 from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound,
-                            rand_weight, to_dtype_np)
+                            rand_weight, record_errors, to_dtype_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -595,6 +595,48 @@ def test_large_scales_round_once(M, mode):
     fin = O.bias_add(pre, None, dtype)
     assert np.isfinite(fin).all()
     assert_output_close(y, pre, fin, dtype, what=f"large scales {mode} M={M}")
+
+
+def _round_significand(v, bits=11):
+    """RNE to `bits` significant bits with no exponent limit (fp16 precision
+    without fp16's range)."""
+    m, e = np.frexp(np.asarray(v, dtype=np.float64))
+    return np.ldexp(np.round(m * 2.0 ** bits) / 2.0 ** bits, e)
+
+
+@pytest.mark.parametrize("M", [1, 16, 20, 40, 64, 100, 130, 520])
+def test_scales_beyond_the_fp16_weight_range(M):
+    """fp16 scales of 600-1500 (|w_eff * s| up to ~1.9e5, past fp16's 65504):
+    the reference's union GEMV keeps w_eff * s in fp32 (grinqh/kernel.py:321-344)
+    and stays finite.  The kernels that round the scaled weight to fp16
+    (17-64-row decode, fused prefill, library GEMM) scale it by 2^-e first and
+    the sums by 2^e, so they compute x @ R(w_eff * s) with R fp16's 11-bit
+    rounding without its range limit; the others keep the product exact."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(900 + M)
+    K, N, b, dtype = 512, 1024, 8, "float16"
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)) * 1e-4, dtype)
+    s = to_dtype_np(np.where(rng.random((K // 128, N)) < 0.5, -1.0, 1.0) * rng.uniform(600, 1500, (K // 128, N)),
+                    dtype)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), _prepare(W, b), _tdt(s, dtype), _tdt(bias, dtype), b, 128, N // 4, t)
+    if rounds_weight(M, dtype):
+        weff = O.effective_weight(W, O.grade(O.union_sigma(x), t, b), b).astype(np.float64)
+        pre = x @ _round_significand(weff * np.repeat(s, 128, axis=0))
+    else:
+        pre = O.gemv_union_f64(x, W, s, t, b, 128)
+    fin = O.bias_add(pre, bias, dtype)
+    assert np.isfinite(fin).all()
+    stats = assert_output_close(y, pre, fin, dtype, bias=bias, what=f"scales past the fp16 weight range M={M}")
+    record_errors("fp16 scales 600-1500", f"M={M}", **stats)
+    # and within the weight-rounding bound of the reference's exact product
+    ref = O.gemv_union_f64(x, W, s, t, b, 128)
+    assert_output_close(y, ref, O.bias_add(ref, bias, dtype), dtype, bias=bias,
+                        extra_tol=dense_rounding_bound(x, W, s, dtype) if rounds_weight(M, dtype) else None,
+                        what=f"scales past the fp16 weight range vs S10, M={M}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

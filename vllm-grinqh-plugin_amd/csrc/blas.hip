@@ -52,9 +52,10 @@ struct GemmShape {
   int64_t M, N, K, ldx;
   int dtype;
   bool bias;
+  bool alpha_vector;  // per-output-column alpha read from device memory
   bool operator==(const GemmShape& o) const {
     return dev == o.dev && M == o.M && N == o.N && K == o.K && ldx == o.ldx && dtype == o.dtype &&
-           bias == o.bias;
+           bias == o.bias && alpha_vector == o.alpha_vector;
   }
 };
 
@@ -89,6 +90,12 @@ bool make_plan(const GemmShape& s, GemmPlan& pl) {
       hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) !=
           HIPBLAS_STATUS_SUCCESS)
     return blas_failed("transpose attributes", -1, s);
+  if (s.alpha_vector) {  // alpha: device vector over the rows of D (the output columns), beta: host
+    const int32_t mode = HIPBLASLT_POINTER_MODE_ALPHA_DEVICE_VECTOR_BETA_HOST;
+    if (hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_POINTER_MODE, &mode, sizeof(mode)) !=
+        HIPBLAS_STATUS_SUCCESS)
+      return blas_failed("pointer mode attribute", -1, s);
+  }
   if (s.bias) {
     const uint32_t epi = HIPBLASLT_EPILOGUE_BIAS;
     const int32_t bdt = dt;
@@ -139,13 +146,13 @@ void destroy_plan(GemmPlan& pl) {
 }  // namespace
 
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
-              int64_t N, int64_t K, int dtype, hipStream_t st) {
+              int64_t N, int64_t K, int dtype, const float* alpha_vec, hipStream_t st) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return GRINQH_ERR_HIP;
   hipblasLtHandle_t h = handle_for_device(dev);
   if (h == nullptr) return GRINQH_ERR_HIP;
   thread_local std::vector<GemmPlan> plans;
-  const GemmShape key{dev, M, N, K, ldx, dtype, bias != nullptr};
+  const GemmShape key{dev, M, N, K, ldx, dtype, bias != nullptr, alpha_vec != nullptr};
   GemmPlan* pl = nullptr;
   for (GemmPlan& q : plans)
     if (q.shape == key) pl = &q;
@@ -167,7 +174,9 @@ int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t
     }
   }
   const float alpha = 1.f, beta = 0.f;
-  const hipblasStatus_t s = hipblasLtMatmul(h, pl->desc, &alpha, wt, pl->a, x, pl->b, &beta, y, pl->d, y, pl->d,
+  const float* pa = alpha_vec != nullptr ? alpha_vec : &alpha;
+  const float* pb = &beta;
+  const hipblasStatus_t s = hipblasLtMatmul(h, pl->desc, pa, wt, pl->a, x, pl->b, pb, y, pl->d, y, pl->d,
                                             &pl->algo, nullptr, 0, st);
   if (s != HIPBLAS_STATUS_SUCCESS) {
     blas_failed("matmul", s, key);

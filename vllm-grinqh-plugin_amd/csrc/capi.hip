@@ -54,7 +54,7 @@ struct WorkspaceLayout {
   // library-GEMM prefill (when either dtype may take it): graded statistic
   // partials and non-finite row flags, then the dense weight [N][K] -- after
   // the regions the fused prefill uses
-  size_t chunk_off, flag_off, wt_off;
+  size_t chunk_off, flag_off, range_off, wt_off;
   bool library_gemm;
   DecodePlan plan;
 };
@@ -99,7 +99,9 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.chunk_off = round_up(w.partial_off + partial, 256);
     w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
-    w.wt_off = w.flag_off + (g ? round_up((size_t)((K + 255) / 256) * (size_t)M, 256) : 0);
+    // graded: the overflow guard's scale-range slots, then the GEMM's alpha vector
+    w.range_off = w.flag_off + (g ? round_up((size_t)((K + 255) / 256) * (size_t)M, 256) : 0);
+    w.wt_off = w.range_off + (g ? round_up((size_t)scale_range_slots(K) * 4, 256) + round_up((size_t)N * 4, 256) : 0);
     w.total = w.wt_off + round_up((size_t)N * (size_t)K * 2, 256);
   }
   return w;
@@ -140,15 +142,22 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
     float* sigma = graded ? reinterpret_cast<float*>(ws + wl.sigma_off) : nullptr;
     uint8_t* flags = reinterpret_cast<uint8_t*>(ws + wl.flag_off);
+    // graded fp16: the overflow guard of the dense weight (scale-range slots, alpha on the device)
+    const bool guard = graded && dtype == GRINQH_DTYPE_F16;
+    uint32_t* slots = guard ? reinterpret_cast<uint32_t*>(ws + wl.range_off) : nullptr;
+    float* alpha =
+        guard ? reinterpret_cast<float*>(ws + wl.range_off + round_up((size_t)scale_range_slots(d.K) * 4, 256))
+              : nullptr;
+    const int64_t n_scale = (int64_t)((d.K + d.gs - 1) / d.gs) * d.N;
     int rc = graded ? launch_sigma_chunks(xs, d.ldx, (int)M, d.K, dtype, reinterpret_cast<float*>(ws + wl.chunk_off),
-                                          flags, sigma, st)
+                                          flags, sigma, guard ? d.scale : nullptr, n_scale, slots, st)
                     : GRINQH_OK;
     if (rc != GRINQH_OK) return rc;
     arm_kernel_timing();
-    rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, st);
+    rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, slots, alpha, st);
     t_kernel_timing = KernelTiming{};
     if (rc == GRINQH_OK)
-      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, st);
+      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, alpha, st);
     if (rc == GRINQH_OK && graded) {
       (void)hipGetLastError();  // the GEMM's library calls may leave one behind as well
       rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);

@@ -101,6 +101,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   __shared__ __align__(16) uint16_t s_bv[RMAX];    // row -> correction-column value
   __shared__ __align__(16) uint32_t s_xm[RMAX];    // row -> zone-0 flip
   __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
+  __shared__ uint32_t s_smax;  // graded scaled path: largest |scale| (fp16 bits) above the overflow limit
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(s_pool);
@@ -123,6 +124,15 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   const int row0 = tile0 * 32;
   const int g_first = row0 / p.gs;
   const int n_groups = (row0 + R - 1) / p.gs - g_first + 1;
+
+  // Graded scaled path: RNE(w * s) overflows fp16 where |w| * |s| > 65504
+  // (|w| <= 2^(2Z-1)), which the reference's fp32 products do not.  A block
+  // whose scales reach past kScaleLimit multiplies them by 2^-e in LDS and its
+  // sums by 2^e (both exact, except for scales that become subnormal).
+  constexpr bool GUARD = SC && !DENSE;
+  constexpr uint32_t kScaleLimit = 0x7BFFu - ((uint32_t)(2 * Z - 1) << 10);  // 65504 / 2^(2Z-1), fp16 bits
+  uint32_t smax = 0;  // largest |scale| bits this thread staged
+  if (GUARD && threadIdx.x == 0) s_smax = 0;
 
   // ---- phase 1a: stage x[:, row0 .. row0+R) and the scales in LDS, all loads in flight at once.
   // Out-of-range buffer offsets read 0: rows m >= M stage as zeros, and nothing past the end of
@@ -166,16 +176,23 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     for (int k = 0; k < SPT; ++k) {
       const int h = tid + NT * k;
       if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
+      if constexpr (GUARD) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) smax = max(smax, max(sv[k][e] & 0x7FFFu, (sv[k][e] >> 16) & 0x7FFFu));
+      }
     }
     if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
       for (int idx = tid; idx < n_groups * 256; idx += NT) {
         const int gl = idx >> 8, col = idx & 255;
         const int wcol = min(w0 + (col & 15), p.NW - 1);
         s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)(col >> 4) * p.NW + wcol];
+        if constexpr (GUARD) smax = max(smax, (uint32_t)s_scale[idx] & 0x7FFFu);
       }
     }
   }
   __syncthreads();
+
+  if (GUARD && smax > kScaleLimit) atomicMax(&s_smax, smax);
 
   // ---- phase 1b: grade each row: correction-column value, zone-0 flip and
   // plane offsets.  Rows with zone 0 active are consumed in offset binary (zone
@@ -209,6 +226,18 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       s_off[rr * Z + z] = ((bits >> z) & 1u) ? row_bytes + (uint32_t)z * (uint32_t)p.NW * 4u : 0x80000000u;
   }
   __syncthreads();
+
+  int up_exp = 0;  // the block's sums are scaled by 2^up_exp at the end
+  if constexpr (GUARD) {
+    const uint32_t hm = s_smax;  // block-uniform
+    if (hm > kScaleLimit) {
+      up_exp = (int)(hm >> 10) - (int)(kScaleLimit >> 10);
+      const float down = __builtin_ldexpf(1.f, -up_exp);
+      for (int idx = tid; idx < n_groups * 256; idx += NT)
+        s_scale[idx] = from_f32<DT>(to_f32<DT>(s_scale[idx]) * down);
+      __syncthreads();
+    }
+  }
 
   // ---- phase 2: main loop over this wave's tiles
   f32x4_t Y[MT][NJ][4];
@@ -416,6 +445,16 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       }
       if (t < t_end) step(t, TA, false, TB);
     }
+  }
+
+  if (GUARD && up_exp > 0) {
+    const float up = __builtin_ldexpf(1.f, up_exp);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) Y[mt][jj][b] *= up;
   }
 
   // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...,

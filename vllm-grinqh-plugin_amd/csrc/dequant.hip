@@ -40,6 +40,9 @@ struct DequantParams {
   const float* sigma;  // graded: union statistic [K]
   GradeThresholds thr;
   int K, N, NW, gs;
+  const uint32_t* slots;  // graded fp16: scale-range slots (overflow guard), else nullptr
+  int n_slots;
+  float* alpha;           // the GEMM's alpha vector [N] when slots != nullptr
 };
 
 constexpr int kDqColsPerBlock = 32;  // plane-word columns per block (4 waves x 8)
@@ -52,6 +55,18 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   __shared__ __align__(16) uint32_t lds[32 * LROW];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cb0 = blockIdx.x * kDqColsPerBlock, kb = blockIdx.y * kDqRowsPerBlock;
+  // overflow guard (graded fp16): the largest |scale| over the slots
+  constexpr bool GUARD = !DENSE && DT::id == F16::id;
+  constexpr uint32_t kScaleLimit = 0x7BFFu - ((uint32_t)(2 * Z - 1) << 10);  // 65504 / 2^(2Z-1), fp16 bits
+  __shared__ uint32_t s_wmax[4];
+  if constexpr (GUARD) {
+    uint32_t hm = 0;
+    if (p.slots != nullptr)
+      for (int i = threadIdx.x; i < p.n_slots; i += 256) hm = max(hm, p.slots[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
+    if (lane == 0) s_wmax[wave] = hm;
+  }
   {  // NW % 4 == 0: a 4-word piece is wholly inside or outside the row
     const int pc = threadIdx.x & 7;  // 4-word piece of the block's 32 columns
 #pragma unroll
@@ -67,6 +82,18 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
     }
   }
   __syncthreads();
+  int up_exp = 0;  // the weight is written times 2^-up_exp and the GEMM's alpha is 2^up_exp
+  if constexpr (GUARD) {
+    const uint32_t hm = max(max(s_wmax[0], s_wmax[1]), max(s_wmax[2], s_wmax[3]));
+    if (hm > kScaleLimit) up_exp = (int)(hm >> 10) - (int)(kScaleLimit >> 10);
+    if (p.alpha != nullptr && blockIdx.y == 0) {  // the block's 16 x 32 output columns
+      const float a = __builtin_ldexpf(1.f, up_exp);
+      for (int i = threadIdx.x; i < 16 * kDqColsPerBlock; i += 256) {
+        const int wcol = cb0 + i % kDqColsPerBlock;
+        if (wcol < p.NW) p.alpha[(int64_t)(i / kDqColsPerBlock) * p.NW + wcol] = a;
+      }
+    }
+  }
   const int c = cb0 + wave * 8 + (lane >> 3);
   const int k0 = kb + 8 * (lane & 7);
   if (c >= p.NW || k0 >= p.K) return;  // K % 32 == 0: a run of 8 rows is whole
@@ -85,6 +112,11 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
   uint16_t sraw[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) sraw[r] = srow[(int64_t)r * p.NW];
+  if (GUARD && up_exp > 0) {
+    const float down = __builtin_ldexpf(1.f, -up_exp);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sraw[r] = from_f32<DT>(to_f32<DT>(sraw[r]) * down);
+  }
 
   int beta[8];  // midpoint bias of each row's zone set (0: every zone active)
 #pragma unroll
@@ -200,10 +232,25 @@ __global__ __launch_bounds__(256) void sigma_chunks_kernel(const uint16_t* __res
 // Second pass: sigma[k] = fmaxf over the chunks' maxima (exact in any order).
 // A block takes 64 columns; its 4 waves take every 4th chunk, 4 loads in
 // flight each, and combine through LDS.
+// With slots != nullptr, block b also writes slots[b] = the largest |value|
+// (fp16 bits) of its share of the n_scale scales (the overflow guard of the
+// graded fp16 dequantization).
 __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* __restrict__ partial, int chunks,
-                                                                  int K, float* __restrict__ sigma) {
+                                                                  int K, float* __restrict__ sigma,
+                                                                  const uint16_t* __restrict__ scale,
+                                                                  int64_t n_scale, uint32_t* __restrict__ slots) {
   __shared__ float s_part[4][64];
+  __shared__ uint32_t s_smax[4];
   const int cl = threadIdx.x & 63, cg = threadIdx.x >> 6;
+  if (slots != nullptr) {
+    const int64_t per = (n_scale + gridDim.x - 1) / gridDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * per, i1 = min(i0 + per, n_scale);
+    uint32_t hm = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) hm = max(hm, (uint32_t)scale[i] & 0x7FFFu);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
+    if (cl == 0) s_smax[cg] = hm;
+  }
   const int k = blockIdx.x * 64 + cl;
   const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
   float s = __int_as_float(0x7fc00000);
@@ -220,6 +267,7 @@ __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* _
   s_part[cg][cl] = s;
   __syncthreads();
   if (cg == 0 && k < K) sigma[k] = fmaxf(fmaxf(s_part[0][cl], s_part[1][cl]), fmaxf(s_part[2][cl], s_part[3][cl]));
+  if (slots != nullptr && threadIdx.x == 0) slots[blockIdx.x] = max(max(s_smax[0], s_smax[1]), max(s_smax[2], s_smax[3]));
 }
 
 // Graded products: a row of x holding a non-finite value has every output
@@ -254,9 +302,10 @@ int launch_dequant_dt(const DequantParams& p, int max_bits, hipStream_t st) {
 }  // namespace
 
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
-                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr, hipStream_t st) {
+                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr,
+                      const uint32_t* slots, float* alpha, hipStream_t st) {
   if (K % 32 != 0 || N % 64 != 0 || gs % 32 != 0 || (int64_t)K * N >= ((int64_t)1 << 40)) return GRINQH_ERR_INVALID;
-  const DequantParams p{planes, scale, wt, sigma, thr, K, N, N / 16, gs};
+  const DequantParams p{planes, scale, wt, sigma, thr, K, N, N / 16, gs, slots, scale_range_slots(K), alpha};
   const bool bf16 = dtype == GRINQH_DTYPE_BF16;
   if (sigma == nullptr)
     return bf16 ? launch_dequant_dt<BF16, true>(p, max_bits, st) : launch_dequant_dt<F16, true>(p, max_bits, st);
@@ -264,7 +313,7 @@ int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* w
 }
 
 int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
-                        float* sigma, hipStream_t st) {
+                        float* sigma, const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st) {
   if (M <= 0 || K <= 0 || K % 8 != 0) return GRINQH_ERR_INVALID;
   const int rows = sigma_chunk_rows(M), chunks = (M + rows - 1) / rows;
   const dim3 grid((unsigned)((K + 255) / 256), (unsigned)chunks);
@@ -272,8 +321,8 @@ int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype,
     hipLaunchKernelGGL(sigma_chunks_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
   else
     hipLaunchKernelGGL(sigma_chunks_kernel<F16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
-  hipLaunchKernelGGL(sigma_chunks_reduce_kernel, dim3((unsigned)((K + 63) / 64)), dim3(256), 0, st, partial, chunks, K,
-                     sigma);
+  hipLaunchKernelGGL(sigma_chunks_reduce_kernel, dim3((unsigned)scale_range_slots(K)), dim3(256), 0, st, partial,
+                     chunks, K, sigma, scale, n_scale, scale != nullptr ? slots : nullptr);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

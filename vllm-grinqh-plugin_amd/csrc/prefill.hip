@@ -81,6 +81,42 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       const_cast<uint16_t*>(p.scale), (short)0, (int)((uint64_t)((p.K + p.gs - 1) / p.gs) * p.N * 2u), 0x00020000);
   const uint32_t s_col_off = ((uint32_t)(4 * j0) * (uint32_t)p.NW + (uint32_t)wc_ld) * 2u;
 
+  // Graded fp16: RNE(w * s) overflows where |w| * |s| > 65504 (|w| <= 2^(2Z-1)),
+  // which the fp32 products of the reference's union GEMV do not.  A block
+  // whose scales (its K range, its 256 columns) reach past kScaleLimit builds
+  // B from s * 2^-e and scales its sums by 2^e (both exact, except for scales
+  // that become subnormal).  Read once before the main loop.
+  constexpr bool GUARD = !DENSE && DT::id == F16::id;
+  constexpr uint32_t kScaleLimit = 0x7BFFu - ((uint32_t)(2 * Z - 1) << 10);  // 65504 / 2^(2Z-1), fp16 bits
+  int up_exp = 0;
+  if constexpr (GUARD) {
+    __shared__ uint32_t s_wmax[WAVES];
+    const int g_lo = (s_begin * BK) / p.gs, g_hi = (s_end * BK - 1) / p.gs;
+    const int total = (g_hi - g_lo + 1) * 256;  // (group, column tile, word column)
+    uint32_t hm = 0;
+    for (int i0 = tid; i0 < total; i0 += NT * 8) {
+      uint16_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int idx = i0 + NT * u;
+        const int col = ((idx >> 4) & 15) * p.NW + min(w0 + (idx & 15), p.NW - 1);
+        const uint32_t off = idx < total ? ((uint32_t)(g_lo + (idx >> 8)) * (uint32_t)p.N + (uint32_t)col) * 2u
+                                         : 0x80000000u;
+        v[u] = __builtin_amdgcn_raw_buffer_load_b16(srsrc, (int)off, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) hm = max(hm, (uint32_t)v[u] & 0x7FFFu);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
+    if (lane == 0) s_wmax[wave] = hm;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) hm = max(hm, s_wmax[w]);
+    if (hm > kScaleLimit) up_exp = (int)(hm >> 10) - (int)(kScaleLimit >> 10);
+  }
+  const float down_scale = __builtin_ldexpf(1.f, -up_exp), up_scale = __builtin_ldexpf(1.f, up_exp);
+
   // registers of one stage's global loads; PD stages are in flight at once
   struct Slot {
     u32x4_t xa[AL];
@@ -146,8 +182,10 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
     if (L.new_group) {
 #pragma unroll
       for (int r = 0; r < 4 * JPT; ++r) {
-        if constexpr (DT::id == F16::id)
-          s2[r] = (uint32_t)L.sraw[r] | ((uint32_t)L.sraw[r] << 16);
+        if constexpr (DT::id == F16::id) {
+          const uint16_t sh = (GUARD && up_exp > 0) ? from_f32<DT>(to_f32<DT>(L.sraw[r]) * down_scale) : L.sraw[r];
+          s2[r] = (uint32_t)sh | ((uint32_t)sh << 16);
+        }
         else
           sf[r] = to_f32<DT>(L.sraw[r]) * (1.0f / (float)(1 << SH));
       }
@@ -326,7 +364,7 @@ __global__ __launch_bounds__(WAVES * 64, OCC) void prefill_kernel(PrefillParams 
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + wm * WM + 16 * i + 4 * q + e;
         if (m >= p.M) continue;
-        const float v = DENSE ? acc[i][r][e] : graded_nonfinite_to_nan(acc[i][r][e]);
+        const float v = DENSE ? acc[i][r][e] : graded_nonfinite_to_nan(GUARD ? acc[i][r][e] * up_scale : acc[i][r][e]);
         if (p.splits == 1)
           p.y[(int64_t)m * p.N + n] = finish_output<DT>(v, p.bias, (int)n);
         else
