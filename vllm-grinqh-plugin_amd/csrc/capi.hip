@@ -16,7 +16,6 @@ namespace {
 
 constexpr int kAbiVersion = 1;
 constexpr int64_t kDecodeMaxRows = 64;     // rows handled by one decode launch
-constexpr int64_t kSigmaPrepassRows = 16;  // graded batches above this reduce sigma in a pre-pass
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -71,7 +70,7 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 }
 
 // [split-K counters (kCounterBytes, zero between calls) | sigma (K floats,
-// graded batches above kSigmaPrepassRows) | split-K partials | library-GEMM
+// graded batches above kDecodeMaxRows) | split-K partials | library-GEMM
 // regions].  The counters sit at offset 0 for every shape, so a workspace
 // shared by calls of different shapes keeps them zero.  The size does not
 // depend on the dtype: when either dtype may take the library path (bf16
@@ -88,7 +87,7 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow
     partial = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
   }
   const bool g = mode == GRINQH_MODE_UNION;
-  const bool need_sigma = g && M > kSigmaPrepassRows;
+  const bool need_sigma = g && M > kDecodeMaxRows;  // the prefill's statistic pass
   w.counter_off = 0;
   w.sigma_off = kCounterBytes;
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
@@ -243,13 +242,7 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   if (graded && sigma_given != nullptr) {  // the producer's chunk maxima (grinqh_*_sigma)
     p.sigma = sigma_given;
     p.sigma_chunks = (int)((M + kSigmaChunkRows - 1) / kSigmaChunkRows);
-  } else if (graded && M > kSigmaPrepassRows) {  // decode above 16 rows grades from the batch statistic
-    float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
-    rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sigma, st);
-    if (rc != GRINQH_OK) return rc;
-    p.sigma = sigma;
-    p.sigma_chunks = 1;
-  }
+  }  // else the GEMV and decode kernels reduce the batch statistic of their rows themselves
   for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
     const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
     const DecodePlan plan = plan_launch(mc, K, N, group_size);

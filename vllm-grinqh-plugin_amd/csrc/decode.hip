@@ -81,10 +81,12 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
   // A operand is read from global memory (L2-resident) with the plane words,
-  // and grading uses the batch statistic computed beforehand, so the K range
-  // is not limited by staging x.
+  // and grading uses the batch statistic of the block's rows, reduced from x
+  // in the prologue (or given by the caller), so the K range is not limited
+  // by staging x.
   constexpr bool AG = MT >= 2;
   constexpr int RMAX = AG ? kDecodeRowsPerBlock : kDecodeRowsPerBlock / MT;
+  static_assert(!AG || RMAX / 8 <= 64 * decode_waves<DT, MT>(), "one statistic chunk per thread");
   constexpr int XS = RMAX + 8;  // halves per staged x row (16-byte rows, banks staggered)
   constexpr int X_BYTES = AG ? 0 : MP * XS * 2;
   constexpr int OFF_BYTES = RMAX * Z * 4;
@@ -102,6 +104,10 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   __shared__ __align__(16) uint32_t s_xm[RMAX];    // row -> zone-0 flip
   __shared__ __align__(16) uint16_t s_scale[SC_GROUPS * 256];  // (group, tile, column) scales
   __shared__ uint32_t s_smax;  // graded scaled path: largest |scale| (fp16 bits) above the overflow limit
+  // above 16 rows, graded, no statistic given: this block's rows of the batch
+  // statistic, max_m |x[m][k]| as float bits (an entry that is NaN in every
+  // row gives 0; every output of such a batch is NaN whatever its grading)
+  __shared__ uint32_t s_sig[AG ? RMAX : 1];
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(s_pool);
@@ -133,6 +139,12 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   constexpr uint32_t kScaleLimit = 0x7BFFu - ((uint32_t)(2 * Z - 1) << 10);  // 65504 / 2^(2Z-1), fp16 bits
   uint32_t smax = 0;  // largest |scale| bits this thread staged
   if (GUARD && threadIdx.x == 0) s_smax = 0;
+  const bool own_sigma = AG && !DENSE && p.sigma == nullptr;  // block-uniform
+  if (own_sigma)
+    for (int i = tid; i < R; i += NT) s_sig[i] = 0u;
+
+  float sig_part[8];  // this thread's maxima of K chunk sig_chunk (-1: none)
+  int sig_chunk = -1;
 
   // ---- phase 1a: stage x[:, row0 .. row0+R) and the scales in LDS, all loads in flight at once.
   // Out-of-range buffer offsets read 0: rows m >= M stage as zeros, and nothing past the end of
@@ -172,6 +184,37 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
         *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
       }
     }
+    // the block's statistic: thread t takes K chunk u0 = t % U (8 rows of K)
+    // for batch rows t / U, t / U + S, ... (U = R / 8 <= NT chunks, S = NT / U
+    // slices), 8 loads at a time
+    if (AG && own_sigma) {
+      const int U = R >> 3, S = NT / U;
+      const int u0 = tid % U, sl = tid / U;
+      if (sl < S) {
+        float mx[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx[e] = 0.f;
+        for (int m0 = sl; m0 < p.M; m0 += 8 * S) {
+          u32x4_t v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int m = m0 + i * S;
+            const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u0) * 2) : 0x80000000u;
+            v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              mx[2 * e] = fmaxf(mx[2 * e], fabsf(to_f32<DT>((uint16_t)(v[i][e] & 0xFFFFu))));
+              mx[2 * e + 1] = fmaxf(mx[2 * e + 1], fabsf(to_f32<DT>((uint16_t)(v[i][e] >> 16))));
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sig_part[e] = mx[e];
+        sig_chunk = u0;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const int h = tid + NT * k;
@@ -193,6 +236,14 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   __syncthreads();
 
   if (GUARD && smax > kScaleLimit) atomicMax(&s_smax, smax);
+  if (AG && own_sigma) {
+    if (sig_chunk >= 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (sig_part[e] > 0.f) atomicMax(&s_sig[8 * sig_chunk + e], __float_as_uint(sig_part[e]));
+    }
+    __syncthreads();
+  }
 
   // ---- phase 1b: grade each row: correction-column value, zone-0 flip and
   // plane offsets.  Rows with zone 0 active are consumed in offset binary (zone
@@ -206,7 +257,9 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       bits = (1u << Z) - 1u;
     } else {
       float s;
-      if (AG || p.sigma != nullptr) {  // batch statistic computed beforehand (always above 16 rows)
+      if (AG && own_sigma) {  // this block's share of the batch statistic
+        s = __uint_as_float(s_sig[rr]);
+      } else if (AG || p.sigma != nullptr) {  // the batch statistic given by the caller
         s = precomputed_sigma(p, row0 + rr);
       } else {
         s = fabsf(to_f32<DT>(s_x[rr]));
