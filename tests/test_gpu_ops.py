@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import grinqh_oracle as O
-from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound,
+from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound, error_stats,
                             rand_weight, record_errors, to_dtype_np)
 
 pytestmark = pytest.mark.gpu
@@ -630,13 +630,16 @@ def test_scales_beyond_the_fp16_weight_range(M):
         pre = O.gemv_union_f64(x, W, s, t, b, 128)
     fin = O.bias_add(pre, bias, dtype)
     assert np.isfinite(fin).all()
-    stats = assert_output_close(y, pre, fin, dtype, bias=bias, what=f"scales past the fp16 weight range M={M}")
-    record_errors("fp16 scales 600-1500", f"M={M}", **stats)
+    assert_output_close(y, pre, fin, dtype, bias=bias, what=f"scales past the fp16 weight range M={M}")
     # and within the weight-rounding bound of the reference's exact product
     ref = O.gemv_union_f64(x, W, s, t, b, 128)
-    assert_output_close(y, ref, O.bias_add(ref, bias, dtype), dtype, bias=bias,
+    ref_fin = O.bias_add(ref, bias, dtype)
+    assert_output_close(y, ref, ref_fin, dtype, bias=bias,
                         extra_tol=dense_rounding_bound(x, W, s, dtype) if rounds_weight(M, dtype) else None,
                         what=f"scales past the fp16 weight range vs S10, M={M}")
+    record_errors("fp16 scales 600-1500 (K=512, N=1024, bias)", f"M={M} union", rows_checked=M,
+                  weight_rounded=rounds_weight(M, dtype), vs_reference=error_stats(y, ref_fin),
+                  vs_own=error_stats(y, fin))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
