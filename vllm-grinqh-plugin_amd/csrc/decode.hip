@@ -146,9 +146,15 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   float sig_part[8];  // this thread's maxima of K chunk sig_chunk (-1: none)
   int sig_chunk = -1;
 
-  // ---- phase 1a: stage x[:, row0 .. row0+R) and the scales in LDS, all loads in flight at once.
-  // Out-of-range buffer offsets read 0: rows m >= M stage as zeros, and nothing past the end of
-  // x or the scale array is touched.
+  // ---- phase 1a: stage x[:, row0 .. row0+R) in LDS (up to 16 rows) or reduce
+  // the block's statistic from it, and load the scales.  The scales are stored
+  // to LDS only once the first tiles' plane loads are issued, so their memory
+  // round trip overlaps those loads; they are loaded after every x load, so
+  // that waiting for x does not wait for them.  Out-of-range buffer offsets
+  // read 0: rows m >= M stage as zeros, and nothing past the end of x or the
+  // scale array is touched.
+  const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
+  u32x4_t sv[SPT];
   {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
@@ -164,18 +170,6 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       const uint32_t off =
           (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
       xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
-    }
-    const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
-    u32x4_t sv[SPT];
-#pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      const int h = tid + NT * k;  // (group, tile, half) chunk
-      const int gl = h >> 5, r = (h >> 1) & 15, hf = h & 1;
-      const uint32_t off =
-          (gl < n_groups && vec_scales)
-              ? (uint32_t)(((int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + w0 + 8 * hf) * 2)
-              : 0x80000000u;
-      sv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(sr, (int)off, 0, 0));
     }
     if constexpr (!AG) {
 #pragma unroll
@@ -217,25 +211,17 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     }
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
-      const int h = tid + NT * k;
-      if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
-      if constexpr (GUARD) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) smax = max(smax, max(sv[k][e] & 0x7FFFu, (sv[k][e] >> 16) & 0x7FFFu));
-      }
-    }
-    if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
-      for (int idx = tid; idx < n_groups * 256; idx += NT) {
-        const int gl = idx >> 8, col = idx & 255;
-        const int wcol = min(w0 + (col & 15), p.NW - 1);
-        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)(col >> 4) * p.NW + wcol];
-        if constexpr (GUARD) smax = max(smax, (uint32_t)s_scale[idx] & 0x7FFFu);
-      }
+      const int h = tid + NT * k;  // (group, tile, half) chunk
+      const int gl = h >> 5, r = (h >> 1) & 15, hf = h & 1;
+      const uint32_t off =
+          (gl < n_groups && vec_scales)
+              ? (uint32_t)(((int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + w0 + 8 * hf) * 2)
+              : 0x80000000u;
+      sv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(sr, (int)off, 0, 0));
     }
   }
   __syncthreads();
 
-  if (GUARD && smax > kScaleLimit) atomicMax(&s_smax, smax);
   if (AG && own_sigma) {
     if (sig_chunk >= 0) {
 #pragma unroll
@@ -251,22 +237,12 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // the 128); other rows have bit 7 clear and need no flip:
   //   w_eff * 2^sh = u + beta * 2^sh - (zone 0 active ? 128 : 0).
   // A row with no active zone therefore contributes exact zeros.
-  for (int rr = tid; rr < R; rr += NT) {
-    uint32_t bits;
-    if (DENSE) {
-      bits = (1u << Z) - 1u;
-    } else {
-      float s;
-      if (AG && own_sigma) {  // this block's share of the batch statistic
-        s = __uint_as_float(s_sig[rr]);
-      } else if (AG || p.sigma != nullptr) {  // the batch statistic given by the caller
-        s = precomputed_sigma(p, row0 + rr);
-      } else {
-        s = fabsf(to_f32<DT>(s_x[rr]));
-        for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
-      }
-      bits = zone_bits<Z>(s, p.thr.t);
-    }
+  // (the loop that reads the caller's statistic from global memory is kept
+  // apart, so that the others have no global load and the scale loads stay in
+  // flight through them)
+  auto grade_row = [&](int rr, float s) {
+    uint32_t bits = (1u << Z) - 1u;
+    if constexpr (!DENSE) bits = zone_bits<Z>(s, p.thr.t);
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
     if constexpr (SC)  // -c_row of the scaled weight (u >> sh) - c_row, an exact fp16 integer
       s_bv[rr] = f32_to_f16_bits(-(float)(1024 + ((bits & 1u) ? (128 >> SH) : 0) - beta));
@@ -277,20 +253,57 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
 #pragma unroll
     for (int z = 0; z < Z; ++z)
       s_off[rr * Z + z] = ((bits >> z) & 1u) ? row_bytes + (uint32_t)z * (uint32_t)p.NW * 4u : 0x80000000u;
+  };
+  if (DENSE) {
+    for (int rr = tid; rr < R; rr += NT) grade_row(rr, 0.f);
+  } else if (AG && own_sigma) {  // this block's share of the batch statistic
+    for (int rr = tid; rr < R; rr += NT) grade_row(rr, __uint_as_float(s_sig[rr]));
+  } else if (AG || p.sigma != nullptr) {  // the batch statistic given by the caller
+    for (int rr = tid; rr < R; rr += NT) grade_row(rr, precomputed_sigma(p, row0 + rr));
+  } else {  // from the staged x
+    for (int rr = tid; rr < R; rr += NT) {
+      float s = fabsf(to_f32<DT>(s_x[rr]));
+      for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
+      grade_row(rr, s);
+    }
   }
   __syncthreads();
 
   int up_exp = 0;  // the block's sums are scaled by 2^up_exp at the end
-  if constexpr (GUARD) {
-    const uint32_t hm = s_smax;  // block-uniform
-    if (hm > kScaleLimit) {
-      up_exp = (int)(hm >> 10) - (int)(kScaleLimit >> 10);
-      const float down = __builtin_ldexpf(1.f, -up_exp);
-      for (int idx = tid; idx < n_groups * 256; idx += NT)
-        s_scale[idx] = from_f32<DT>(to_f32<DT>(s_scale[idx]) * down);
-      __syncthreads();
+  // The scales into LDS, once the first tiles' plane loads are issued; then
+  // the overflow guard.  The barriers carry no memory fence, so they do not
+  // wait for those plane loads, only for the LDS accesses before them.
+  auto stage_scales = [&]() {
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + NT * k;
+      if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
+      if constexpr (GUARD) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) smax = max(smax, max(sv[k][e] & 0x7FFFu, (sv[k][e] >> 16) & 0x7FFFu));
+      }
     }
-  }
+    if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
+      for (int idx = tid; idx < n_groups * 256; idx += NT) {
+        const int gl = idx >> 8, col = idx & 255;
+        const int wcol = min(w0 + (col & 15), p.NW - 1);
+        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)(col >> 4) * p.NW + wcol];
+        if constexpr (GUARD) smax = max(smax, (uint32_t)s_scale[idx] & 0x7FFFu);
+      }
+    }
+    if (GUARD && smax > kScaleLimit) atomicMax(&s_smax, smax);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if constexpr (GUARD) {
+      const uint32_t hm = s_smax;  // block-uniform
+      if (hm > kScaleLimit) {
+        up_exp = (int)(hm >> 10) - (int)(kScaleLimit >> 10);
+        const float down = __builtin_ldexpf(1.f, -up_exp);
+        for (int idx = tid; idx < n_groups * 256; idx += NT)
+          s_scale[idx] = from_f32<DT>(to_f32<DT>(s_scale[idx]) * down);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    }
+  };
 
   // ---- phase 2: main loop over this wave's tiles
   f32x4_t Y[MT][NJ][4];
@@ -481,6 +494,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
       issue(t_begin, TA);
       issue(t_begin + 1, TB);
+      stage_scales();
       for (; t + 3 <= t_end; t += 3) {
         step(t, TA, true, TC);
         step(t + 1, TB, true, TA);
@@ -492,6 +506,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     } else {
       // two tile buffers: tile t+1 is in flight while tile t is unpacked
       issue(t_begin, TA);
+      stage_scales();
       for (; t + 2 <= t_end; t += 2) {
         step(t, TA, true, TB);
         step(t + 1, TB, true, TA);

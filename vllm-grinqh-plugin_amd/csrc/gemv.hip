@@ -98,8 +98,12 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   const bool col_ok = (w0 + lane) < p.NW;
   const int wc = col_ok ? (w0 + lane) : (p.NW - 1);
 
-  // ---- phase 1a: stage x rows 0..3 of [row0, row0 + R) and the scales; loads first, then stores.
-  // Out-of-range offsets read 0: rows m >= M stage as zeros.
+  // ---- phase 1a: stage x rows 0..3 of [row0, row0 + R); the scales are loaded
+  // here and stored to LDS only once the first tiles' plane loads are issued
+  // (they are needed at the first group's end), so their memory round trip
+  // overlaps those loads.  Out-of-range offsets read 0: rows m >= M stage as zeros.
+  const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
+  u32x4_t sv[SPT];
   {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
@@ -114,8 +118,6 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
           (m < p.M && 8 * u < R) ? (uint32_t)(((int64_t)m * p.ldx + row0 + 8 * u) * 2) : 0x80000000u;
       xv[k] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0));
     }
-    const bool vec_scales = (p.NW % 8) == 0 && (reinterpret_cast<uintptr_t>(p.scale) & 15u) == 0;
-    u32x4_t sv[SPT];
 #pragma unroll
     for (int k = 0; k < SPT; ++k) {
       const int h = tid + 256 * k;
@@ -132,38 +134,18 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
       *reinterpret_cast<u32x4_t*>(&s_x[m * XS + 8 * u]) = xv[k];
     }
     if (tid < CPR) *reinterpret_cast<u32x4_t*>(&s_x[4 * XS + 8 * tid]) = u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      const int h = tid + 256 * k;
-      if (h < SCH) *reinterpret_cast<u32x4_t*>(&s_scale[h * 8]) = sv[k];
-    }
-    if (!vec_scales) {  // element-wise staging
-      for (int idx = tid; idx < n_groups * 1024; idx += 256) {
-        const int gl = idx >> 10, r = (idx >> 6) & 15;
-        const int wcol = min(w0 + (idx & 63), p.NW - 1);
-        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + wcol];
-      }
-    }
   }
   __syncthreads();
 
   // ---- phase 1b: grade each row: correction-column value, zone-0 flip and plane
   // offsets (w_eff * 2^sh = u + beta * 2^sh - (zone 0 active ? 128 : 0), with u the
-  // offset-binary byte when zone 0 is active, else U & mask)
-  for (int rr = tid; rr < R; rr += 256) {
-    uint32_t bits;
-    if (DENSE) {
-      bits = (1u << Z) - 1u;
-    } else {
-      float s;
-      if (p.sigma != nullptr) {  // statistic of a whole batch split into several launches
-        s = precomputed_sigma(p, row0 + rr);
-      } else {
-        s = fabsf(to_f32<DT>(s_x[rr]));
-        for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
-      }
-      bits = zone_bits<Z>(s, p.thr.t);
-    }
+  // offset-binary byte when zone 0 is active, else U & mask).  The statistic
+  // comes from the staged x, or from the caller (a batch split into several
+  // launches, a producer's chunk maxima); the two loops are separate so that
+  // the first has no global load, and the scale loads stay in flight through it.
+  auto grade_row = [&](int rr, float s) {
+    uint32_t bits = (1u << Z) - 1u;
+    if constexpr (!DENSE) bits = zone_bits<Z>(s, p.thr.t);
     const int beta = DENSE ? 0 : midpoint_bias<Z>(bits);
     s_bv[rr] = BOperand<DT>::correction(beta * (1 << SH) - ((bits & 1u) ? 128 : 0));
     s_xm[rr] = zone0_flip(bits);
@@ -171,6 +153,18 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
 #pragma unroll
     for (int z = 0; z < Z; ++z)
       s_off[rr * Z + z] = ((bits >> z) & 1u) ? row_bytes + (uint32_t)z * (uint32_t)p.NW * 4u : 0x80000000u;
+  };
+  if (DENSE || p.sigma == nullptr) {
+    for (int rr = tid; rr < R; rr += 256) {
+      float s = 0.f;
+      if constexpr (!DENSE) {
+        s = fabsf(to_f32<DT>(s_x[rr]));
+        for (int m = 1; m < p.M; ++m) s = fmaxf(s, fabsf(to_f32<DT>(s_x[m * XS + rr])));
+      }
+      grade_row(rr, s);
+    }
+  } else {
+    for (int rr = tid; rr < R; rr += 256) grade_row(rr, precomputed_sigma(p, row0 + rr));
   }
   __syncthreads();
 
@@ -287,6 +281,21 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     uint32_t DA[TR][Z], DB[TR][Z], DC[TR][Z];
     issue(t_begin, DA);
     issue(t_begin + 1, DB);
+    // the scales, now that the first tiles' loads are in flight; the barrier
+    // does not wait for those loads (no memory fence), only for the LDS stores
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int h = tid + 256 * k;
+      if (h < SCH) *reinterpret_cast<u32x4_t*>(&s_scale[h * 8]) = sv[k];
+    }
+    if (!vec_scales) {  // element-wise staging
+      for (int idx = tid; idx < n_groups * 1024; idx += 256) {
+        const int gl = idx >> 10, r = (idx >> 6) & 15;
+        const int wcol = min(w0 + (idx & 63), p.NW - 1);
+        s_scale[idx] = p.scale[(int64_t)(g_first + gl) * p.N + (int64_t)r * p.NW + wcol];
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     int t = t_begin;
     for (; t + 3 <= t_end; t += 3) {
       step(t, DA, true, DC);
