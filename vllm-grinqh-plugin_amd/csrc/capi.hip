@@ -129,9 +129,10 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // larger activations.
 bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64_t)1 << 31); }
 
-// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm), else one fused
-// prefill launch over the whole batch (graded batches
-// first reduce the union statistic over all M rows).
+// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm), else one
+// prefill launch over the whole batch, the wide-tile kernel where it applies
+// (prefill_wide_applies) or the fused prefill kernel (graded batches first
+// reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
   if (wl.library_gemm && use_library_gemm(M, d.N, dtype)) {  // the (graded) weight once, then the library GEMM
@@ -164,6 +165,9 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     return rc;
   }
   if (!x_fits_fused_prefill(M, d.ldx)) return GRINQH_ERR_INVALID;  // x of 2 GiB or more: split the batch
+  // without the library path (allocation-free entry point): the wide-tile
+  // kernel where its grid fills the GPU, else the fused prefill kernel
+  const bool wide = prefill_wide_applies(M, d.K, d.N, d.ldx, d.gs, dtype);
   PrefillParams p{};
   p.x = xs;
   p.ldx = d.ldx;
@@ -178,7 +182,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   p.NW = d.NW;
   p.gs = d.gs;
   p.sigma = nullptr;
-  p.splits = prefill_splits(M, d.K, d.N);
+  p.splits = wide ? 1 : prefill_splits(M, d.K, d.N);
   p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
   if (graded) {  // the batch statistic the rows are graded on
     float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
@@ -188,7 +192,8 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
   }
   arm_kernel_timing();
   int splits_run = 1;
-  int rc = launch_prefill(p, max_bits, dtype, !graded, st, &splits_run);
+  int rc = wide ? launch_prefill_wide(p, max_bits, !graded, st)
+                : launch_prefill(p, max_bits, dtype, !graded, st, &splits_run);
   t_kernel_timing = KernelTiming{};
   if (rc != GRINQH_OK) return rc;
   if (splits_run > 1) {  // add the K ranges in order, cast, bias

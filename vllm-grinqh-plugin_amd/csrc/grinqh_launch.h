@@ -105,6 +105,19 @@ int prefill_block_rows(int64_t M, int64_t N);
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
 
+// Large-batch fp16 prefill without the library path (prefill_wide.hip):
+// 256 x 256 output tiles, the weight dequantized into LDS per 64-row stage.
+// From kWidePrefillRows rows, N % 256 == 0, K and the group size multiples of
+// 64, (M + 256) * ldx * 2 < 2^31, and at least kWideMinTiles tiles: one block
+// per CU, so smaller grids leave CUs idle and the fused kernel's 128-row tiles
+// are faster (o_proj at 2048 rows: 128 tiles, 164 against 125 us; qkv: 192
+// tiles, 172 against 235 us).
+constexpr int64_t kWidePrefillRows = 512;
+constexpr int64_t kWideMinTiles = 192;
+bool prefill_wide_applies(int64_t M, int64_t K, int64_t N, int64_t ldx, int gs, int dtype);
+// one launch over the whole K range (p.splits, p.partial unused)
+int launch_prefill_wide(const PrefillParams& p, int max_bits, bool dense, hipStream_t st);
+
 // Prefill from kLibraryGemmRows rows (and N % 64 == 0): the weight Wt[N][K] =
 // RNE(w * s) (graded: RNE(w_eff * s) from the union statistic) is written
 // once (dequant.hip), then a library GEMM multiplies it (blas.hip); below,
