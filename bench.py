@@ -19,9 +19,11 @@ by the grading + scales + x + y) per second.  The JSON line also carries the
 per-case product times, the roofline of the dominant kernel, the prefill
 TFLOP/s at M=2048 (dense, the reference's dispatch for M > 1), the graded
 prefill sweep of BASELINE configs[2] (M = 512, 2048, 8192, 70/20/8/2 % grade
-mix), the Llama-3-70B shapes of BASELINE configs[4] with every zone active
-(M = 1, 64, 4096) and the CPU baseline (the reference's pure-PyTorch math on
-the host cores).
+mix), the M=2048 products without the library path (allocation-free entry
+point: the hand-written wide-tile kernel instead of the dense weight and the
+library GEMM), the Llama-3-70B shapes of BASELINE configs[4] with every zone
+active (M = 1, 64, 4096) and the CPU baseline (the reference's pure-PyTorch
+math on the host cores).
 """
 from __future__ import annotations
 
@@ -82,6 +84,23 @@ def synth_x(torch, M: int, K: int, seed: int, device):
 def thresholds_for(x, q=(0.5, 0.8, 0.95)):
     sigma = x.abs().float().amax(0).cpu().numpy()
     return [0.0] + [float(v) for v in np.quantile(sigma, q)]
+
+
+def library_free_product(torch, lib, x, P, s, t, mode):
+    """One product through grinqh_gemm_or_gemv_noalloc (include/grinqh.h): no
+    workspace, so no dense weight for the library GEMM; fp16 batches of 512
+    rows and more run the wide-tile prefill kernel where its grid fills the
+    GPU, else the fused prefill kernel."""
+    from grinqh import _lib
+    M, K = x.shape
+    N = s.shape[1]
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    rc = lib.grinqh_gemm_or_gemv_noalloc(
+        x.data_ptr(), M, K, x.stride(0), N, _lib.DTYPE_F16, P.data_ptr(), s.data_ptr(), None, y.data_ptr(), BITS,
+        GS, _lib.thresholds_f32(t), _lib.MODE_UNION if mode == "union" else _lib.MODE_DENSE,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "grinqh_gemm_or_gemv_noalloc")
+    return y
 
 
 class ColdRotation:
@@ -356,9 +375,12 @@ def main() -> int:
     ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B shape sweep (BASELINE configs[4])")
     ap.add_argument("--no-model-step", action="store_true",
                     help="skip the Llama-3-8B decode-step stand-in (BASELINE configs[3])")
-    ap.add_argument("--prefill-case", default=None, metavar="SHAPE:M:MODE",
+    ap.add_argument("--prefill-case", default=None, metavar="SHAPE:M:MODE[:noalloc]",
                     help="profiling run: one prefill product (e.g. gate_up:2048:union; MODE dense or union with "
-                         "t = [0, P70, P90, P98]) twice as warm-up and twice counted; prints no JSON line")
+                         "t = [0, P70, P90, P98]; ':noalloc' through the allocation-free entry point, i.e. without "
+                         "the library path) twice as warm-up and twice counted; prints no JSON line")
+    ap.add_argument("--no-library-free", action="store_true",
+                    help="skip the prefill products through the allocation-free entry point (no library path)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter-collection run: each decode case twice (eager, cold weight copies) and a 256 MiB "
                          "copy kernel of known traffic for calibrating FETCH_SIZE / WRITE_SIZE; prints no JSON line")
@@ -379,24 +401,29 @@ def main() -> int:
     log(f"device {torch.cuda.get_device_name(dev)}")
 
     if args.prefill_case:
-        name, m_str, mode = args.prefill_case.split(":")
+        name, m_str, mode, *path = args.prefill_case.split(":")
         K, N = {n: (k, nn) for n, k, nn in SHAPES}[name]
         M = int(m_str)
         w, s = synth_weight(torch, K, N, 1000, dev)
         P = prepare_weight(w, BITS)
         x = synth_x(torch, M, K, 5, dev)
         t = thresholds_for(x, (0.7, 0.9, 0.98)) if mode == "union" else [0.0] * 4
+        if path == ["noalloc"]:
+            lib = _lib.load_library()
+            call = lambda: library_free_product(torch, lib, x, P, s, t, mode)
+        else:
+            call = lambda: run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
         for _ in range(2):
-            run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
+            call()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(2):
-            run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
+            call()
         e1.record()
         e1.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / 2
-        log(f"prefill case {name} M={M} {mode}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s")
+        log(f"prefill case {args.prefill_case}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s")
         return 0
 
     # ---------------- weights: a pool of >= POOL_BYTES of copies per shape, handed out LRU
@@ -593,6 +620,38 @@ def main() -> int:
                                        "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
                 log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
                 del x
+    # ---------------- the same products without the library path (allocation-free
+    # entry point: no dense weight; the wide-tile kernel where its grid fills the
+    # GPU), eager, rotated copies
+    prefill_library_free = None
+    if not args.no_prefill and not args.no_library_free:
+        prefill_library_free = []
+        lib = _lib.load_library()
+        for i, (name, K, N) in enumerate(SHAPES):
+            for M, mode in ((PREFILL_M, "dense"), (PREFILL_M, "union")):
+                x = synth_x(torch, M, K, 299 + i, dev)
+                t = thresholds_for(x, (0.7, 0.9, 0.98)) if mode == "union" else [0.0] * 4
+                touched = K * N * BITS // 8 + (K // GS) * N * 2
+                n_it = min(len(pools[name]), 8)
+                for _ in range(2):
+                    P, sc = rot.take(name, touched)
+                    library_free_product(torch, lib, x, P, sc, t, mode)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(n_it):
+                    P, sc = rot.take(name, touched)
+                    library_free_product(torch, lib, x, P, sc, t, mode)
+                e1.record()
+                e1.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / n_it
+                tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
+                kernel = "prefill_wide_kernel" if (N // 256) * -(-M // 256) >= 192 else "prefill_kernel"
+                prefill_library_free.append({"shape": name, "M": M, "mode": mode, "us": round(us, 2),
+                                             "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                             "kernel": kernel})
+                log(f"prefill library-free {name:8s} M={M} {mode:5s} {us:9.1f} us {tf:7.1f} TFLOP/s ({kernel})")
+                del x
     prefill_min_gap = rot.min_gap
     del pools, rot
     torch.cuda.empty_cache()
@@ -718,6 +777,7 @@ def main() -> int:
                    if k not in ("x", "t", "touched")} for c in cases],
         "prefill": prefill,
         "prefill_graded": prefill_graded,
+        "prefill_library_free": prefill_library_free,
         "llama70b_adversarial": big,
         "llama8b_decode_step": model_step,
     }
