@@ -153,11 +153,15 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
                                           flags, sigma, guard ? d.scale : nullptr, n_scale, slots, st)
                     : GRINQH_OK;
     if (rc != GRINQH_OK) return rc;
+    auto dequant = [&](hipStream_t s) {
+      return launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, slots, alpha, s);
+    };
     arm_kernel_timing();
-    rc = launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, slots, alpha, st);
+    rc = dequant(st);
     t_kernel_timing = KernelTiming{};
+    const GemmPrelude prelude = dequant;
     if (rc == GRINQH_OK)
-      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, alpha, st);
+      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, alpha, st, &prelude);
     if (rc == GRINQH_OK && graded) {
       (void)hipGetLastError();  // the GEMM's library calls may leave one behind as well
       rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <functional>
+
 #include "grinqh.h"
 
 namespace grinqh {
@@ -175,9 +177,14 @@ int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype,
 int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st);
 // y[m][n] = alpha[n] * (x[M][K] @ wt[N][K]^T)[m][n] (+ bias[n]) in the
 // activation dtype, fp32 accumulation; alpha = 1, or the N-vector alpha read
-// by the GEMM from device memory
+// by the GEMM from device memory.  The first call of a shape times the
+// library's candidate algorithms; prelude (optional) enqueues on a given
+// stream the work that precedes the GEMM in the product (the dequantization
+// of wt), run before each timed candidate.
+using GemmPrelude = std::function<int(hipStream_t)>;
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
-              int64_t N, int64_t K, int dtype, const float* alpha, hipStream_t st);
+              int64_t N, int64_t K, int dtype, const float* alpha, hipStream_t st,
+              const GemmPrelude* prelude = nullptr);
 
 
 // Benchmark timing of a product's main kernel: when armed (by
