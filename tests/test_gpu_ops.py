@@ -642,6 +642,32 @@ def test_scales_beyond_the_fp16_weight_range(M):
                   vs_own=error_stats(y, fin))
 
 
+def test_library_graded_scales_not_16_byte_aligned():
+    """The graded library path's statistic pass scans the scales for the fp16
+    overflow guard with 16-byte loads when the scale array is 16-byte aligned
+    and element by element otherwise: a scale tensor two bytes off alignment
+    (a view into a larger buffer), with scales past fp16's weight range so
+    that the guard acts, gives the same output bit for bit."""
+    from grinqh.kernel import grinqh_gemv_batch_union
+    rng = np.random.default_rng(913)
+    M, K, N, b = 520, 512, 1024, 8
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)) * 1e-4, "float16")
+    s = to_dtype_np(np.where(rng.random((K // 128, N)) < 0.5, -1.0, 1.0) * rng.uniform(600, 1500, (K // 128, N)),
+                    "float16")
+    t = [0.0] + np.quantile(O.union_sigma(x), [0.5, 0.8, 0.95]).tolist()
+    P, xt = _prepare(W, b), _tdt(x, "float16")
+    st = _tdt(s, "float16")
+    buf = torch.empty(st.numel() + 8, dtype=torch.float16, device=st.device)
+    sv = buf[1:1 + st.numel()].view(st.shape)
+    sv.copy_(st)
+    assert sv.data_ptr() % 16 == 2
+    y0 = grinqh_gemv_batch_union(xt, P, st, None, b, 128, N // 4, t)
+    y1 = grinqh_gemv_batch_union(xt, P, sv, None, b, 128, N // 4, t)
+    assert torch.isfinite(y0.float()).all()
+    assert torch.equal(y0, y1)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M", [1, 3, 20, 40, 64, 100, 520])
 def test_nonfinite_rows_poison_their_output_row(M, dtype):

@@ -243,10 +243,27 @@ __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* _
   __shared__ uint32_t s_smax[4];
   const int cl = threadIdx.x & 63, cg = threadIdx.x >> 6;
   if (slots != nullptr) {
-    const int64_t per = (n_scale + gridDim.x - 1) / gridDim.x;
-    const int64_t i0 = (int64_t)blockIdx.x * per, i1 = min(i0 + per, n_scale);
+    // each block's share of the scales (whole 16-byte vectors when the
+    // array is 16-byte aligned), four vectors per thread in flight
+    const int64_t per = ((n_scale + gridDim.x - 1) / gridDim.x + 7) & ~(int64_t)7;
+    const int64_t i0 = min((int64_t)blockIdx.x * per, n_scale), i1 = min(i0 + per, n_scale);
     uint32_t hm = 0;
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) hm = max(hm, (uint32_t)scale[i] & 0x7FFFu);
+    int64_t tail = i0;
+    if ((reinterpret_cast<uintptr_t>(scale) & 15u) == 0) {
+      const int64_t nv = (i1 - i0) / 8;
+      const u32x4_t* sv = reinterpret_cast<const u32x4_t*>(scale + i0);
+      for (int64_t j = threadIdx.x; j < nv; j += 4 * 256) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = j + 256 * u < nv ? sv[j + 256 * u] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) hm = max(hm, max(v[u][q] & 0x7FFFu, (v[u][q] >> 16) & 0x7FFFu));
+      }
+      tail = i0 + 8 * nv;
+    }
+    for (int64_t i = tail + threadIdx.x; i < i1; i += 256) hm = max(hm, (uint32_t)scale[i] & 0x7FFFu);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
     if (cl == 0) s_smax[cg] = hm;
