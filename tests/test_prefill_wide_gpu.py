@@ -80,6 +80,31 @@ def test_wide_prefill_dense(lib, max_bits):
                   rows_checked=M, weight_rounded=True, vs_reference=error_stats(y, fin), vs_own=error_stats(y, fin))
 
 
+@pytest.mark.parametrize("group_size", [64, 256])
+def test_wide_prefill_group_sizes(lib, group_size):
+    """Scale groups of 64 rows (a new group every 64-row stage) and of 256
+    rows (one group over four stages), dense, K = 1024, 512 rows, bias."""
+    from grinqh.utils import prepare_weight
+    rng = np.random.default_rng(5700 + group_size)
+    M, K, N, b = 512, 1024, 24576, 8
+    W = rand_weight(rng, K, N, b)
+    s = to_dtype_np(rng.standard_normal((K // group_size, N)) * 0.02, "float16")
+    P = prepare_weight(torch.from_numpy(W).cuda(), b)
+    x = to_dtype_np(rng.standard_normal((M, K)), "float16")
+    bias = to_dtype_np(rng.standard_normal(N), "float16")
+    from grinqh import _lib
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    xt, st, bt = _dev(x), _dev(s), _dev(bias)
+    rc = lib.grinqh_gemm_or_gemv_noalloc(
+        xt.data_ptr(), M, K, xt.stride(0), N, _lib.DTYPE_F16, P.data_ptr(), st.data_ptr(), bt.data_ptr(),
+        y.data_ptr(), b, group_size, _lib.thresholds_f32([0.0] * 4), _lib.MODE_DENSE,
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "grinqh_gemm_or_gemv_noalloc")
+    pre = O.dense_prefill_f64(x, W, s, group_size, "float16")
+    fin = O.dense_prefill(x, W, s, bias, group_size, "float16")
+    assert_output_close(y, pre, fin, "float16", bias=bias, what=f"wide prefill group size {group_size}")
+
+
 @pytest.mark.parametrize("max_bits", [4, 8])
 @pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0], None],
                          ids=["non_monotone", "skip_all", "all_planes", "tied", "quantiles"])
