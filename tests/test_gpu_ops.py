@@ -366,6 +366,29 @@ def test_prefill_library_gemm(M, K, N, max_bits, dtype):
                         what=f"library prefill {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("mode", ["dense", "union"])
+def test_library_gemm_size_class_reuses_timed_choice(mode):
+    """The library GEMM's algorithm is timed once per size class (rows
+    rounded up to a power of two): 520 rows time the candidates, 1000 rows
+    (the same class) take the same algorithm when the library offers it for
+    that size.  Both products are held to the oracle."""
+    from grinqh.kernel import run_product
+    rng = np.random.default_rng(4711 if mode == "dense" else 4712)
+    K, N, b = 512, 2304, 8
+    W = rand_weight(rng, K, N, b)
+    s = to_dtype_np(rng.standard_normal((K // 128, N)) * 0.05, "float16")
+    P, st = _prepare(W, b), _tdt(s, "float16")
+    for M in (520, 1000):
+        x = to_dtype_np(rng.standard_normal((M, K)), "float16")
+        t = [0.0] + np.quantile(O.union_sigma(x), [0.7, 0.9, 0.98]).tolist() if mode == "union" else [0.0] * 4
+        y = run_product(_tdt(x, "float16"), P, st, None, b, 128, N // 4, t, mode)
+        if mode == "dense":
+            pre = O.dense_prefill_f64(x, W, s, 128, "float16")
+        else:
+            pre = O.gemv_union_rounded_f64(x, W, s, t, b, 128, "float16")
+        assert_output_close(y, pre, O.bias_add(pre, None, "float16"), "float16", what=f"library {mode} M={M}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("max_bits", [4, 8])
 @pytest.mark.parametrize("t", [[0.5, 0.1, 2.0, 1.0], [float("inf")] * 4, [-1.0] * 4, [0.0, 0.2, 0.2, 3.0], None],

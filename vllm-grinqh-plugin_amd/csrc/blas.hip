@@ -14,10 +14,11 @@
 // One hipBLASLt handle per device (created on first use, kept for the
 // process); the descriptors and the chosen algorithm of each shape are
 // cached per thread, so a call after the first only sets the bias pointer and
-// enqueues the GEMM.  The first call of a shape times the heuristic's
-// candidates in the product's own sequence (fastest_candidate) and keeps the
-// fastest: gate_up at 2048 rows 465 -> 428 us for the whole product, gate_up
-// and down at 8192 rows ~20 % faster, the other Llama-3-8B shapes unchanged.
+// enqueues the GEMM.  The first call of a size class (M rounded up to a power
+// of two) times the heuristic's candidates in the product's own sequence
+// (fastest_candidate) and keeps the fastest: gate_up at 2048 rows 465 -> 428
+// us for the whole product, gate_up and down at 8192 rows ~20 % faster, the
+// other Llama-3-8B shapes unchanged.
 //
 // Only algorithms that use no workspace are taken.  The stream-K algorithms
 // the heuristic prefers for the large shapes use one, and a graded gate_up
@@ -27,6 +28,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -76,6 +78,18 @@ bool blas_failed(const char* what, int status, const GemmShape& s) {
                status, (long long)s.M, (long long)s.N, (long long)s.K, (long long)s.ldx, s.dtype);
   return false;
 }
+
+// Size class of a timed algorithm choice.
+struct TuneKey {
+  int dev;
+  int64_t m_bucket, N, K;
+  int dtype;
+  bool bias, alpha_vector;
+  bool operator==(const TuneKey& o) const {
+    return dev == o.dev && m_bucket == o.m_bucket && N == o.N && K == o.K && dtype == o.dtype && bias == o.bias &&
+           alpha_vector == o.alpha_vector;
+  }
+};
 
 // Operands of the call that creates a plan, for timing its candidates.
 struct GemmCall {
@@ -214,9 +228,29 @@ bool make_plan(const GemmShape& s, GemmPlan& pl, const GemmCall& call) {
   for (int i = 0; i < found && i < kCandidates; ++i)
     if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0) algos[n++] = res[i].algo;
   if (n == 0) return blas_failed("heuristic (no candidate without workspace)", -3, s);
+  // The timed choice is kept per size class: M rounded up to a power of two
+  // (with N, K, dtype and epilogue).  Another M of the class takes the same
+  // algorithm when its own candidate list holds it, else its first candidate,
+  // so that a new batch size does not time the candidates again.
+  int64_t mb = 1;
+  while (mb < s.M) mb <<= 1;
+  const TuneKey tk{s.dev, mb, s.N, s.K, s.dtype, s.bias, s.alpha_vector};
+  thread_local std::vector<std::pair<TuneKey, hipblasLtMatmulAlgo_t>> tuned;
+  for (const auto& e : tuned) {
+    if (!(e.first == tk)) continue;
+    pl.algo = algos[0];
+    for (int i = 0; i < n; ++i)
+      if (std::memcmp(algos[i].data, e.second.data, sizeof(e.second.data)) == 0) pl.algo = algos[i];
+    return true;
+  }
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(call.stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-  pl.algo = algos[cap == hipStreamCaptureStatusNone ? fastest_candidate(pl, algos, n < kTimedCandidates ? n : kTimedCandidates, call) : 0];
+  if (cap != hipStreamCaptureStatusNone) {  // nothing is timed during a capture (nor remembered)
+    pl.algo = algos[0];
+    return true;
+  }
+  pl.algo = algos[fastest_candidate(pl, algos, n < kTimedCandidates ? n : kTimedCandidates, call)];
+  tuned.emplace_back(tk, pl.algo);
   return true;
 }
 
