@@ -620,6 +620,16 @@ def main() -> int:
                                        "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
                 log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
                 del x
+    # MFMA leg of the metric (M=2048): the largest product, gate_up, priced on
+    # its whole graph-timed time (dequantization pass + library GEMM; the
+    # kernels' own times are in profiles/prefill_gate_up_m2048_kernel_stats.md)
+    roofline_prefill = None
+    if prefill:
+        g = max(prefill, key=lambda r: r["us"])
+        roofline_prefill = {"bound": "mfma", "achieved": g["tflops"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": g["frac"], "traffic": None, "shape": g["shape"], "M": g["M"],
+                            "measured": "graph-timed product: dequantization pass + library GEMM, rotated weights"}
+
     # ---------------- the same products without the library path (allocation-free
     # entry point: no dense weight; the wide-tile kernel where its grid fills the
     # GPU), eager, rotated copies
@@ -777,6 +787,7 @@ def main() -> int:
                    if k not in ("x", "t", "touched")} for c in cases],
         "prefill": prefill,
         "prefill_graded": prefill_graded,
+        "roofline_prefill": roofline_prefill,
         "prefill_library_free": prefill_library_free,
         "llama70b_adversarial": big,
         "llama8b_decode_step": model_step,
