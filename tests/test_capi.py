@@ -62,9 +62,9 @@ def test_workspace_query_library_gemm_path(lib):
     the workspace for the K-contiguous weight (2*N*K bytes) after the fused
     kernel's regions (the GEMM itself takes no workspace).  The query has no dtype, so it
     covers the path whenever either dtype may take it: from 512 rows, from
-    224 in bf16, at 257-511 rows when the fused grid would need more than one
-    round (gate_up's N); never when N / 16 is not a multiple of 4; dense and
-    union alike."""
+    224 in bf16, at 257-511 rows when K <= 8192 or the fused grid would need
+    more than one round (gate_up's N); never when N / 16 is not a multiple of
+    4; dense and union alike."""
     K = 4096
     dense, union = 2, 1
     library = lambda M, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode) >= 2 * N * K

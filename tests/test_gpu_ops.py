@@ -268,7 +268,7 @@ def test_union_graded_batches(M, max_bits, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("max_bits", BITS)
-@pytest.mark.parametrize("M,K,N", [(65, 256, 320), (300, 512, 768), (129, 96, 4112), (100, 32, 256), (100, 64, 256),
+@pytest.mark.parametrize("M,K,N", [(65, 256, 320), (300, 512, 784), (129, 96, 4112), (100, 32, 256), (100, 64, 256),
                                    (100, 128, 256)])
 def test_prefill_dense_shapes(M, K, N, max_bits, dtype):
     """Prefill kernel (more than 64 rows) against S9 with bias: partial row
@@ -348,8 +348,8 @@ def test_prefill_256_row_tiles(dtype):
 @pytest.mark.parametrize("M,K,N", [(512, 96, 256), (700, 512, 768), (512, 2080, 320), (600, 256, 4112),
                                    (300, 256, 28672)])
 def test_prefill_library_gemm(M, K, N, max_bits, dtype):
-    """Dense batches of 512 rows and more, and of 257-511 rows when the fused
-    grid would need more than one round (300 x 28672): the dense weight
+    """Dense batches of 512 rows and more, and of 257-511 rows when K <= 8192
+    or the fused grid would need more than one round (300 x 28672): the dense weight
     Wt[N][K] is written once (dequant kernel: 64-row tiles, the last one
     partial when K % 64 == 32; scale groups of 128 crossing tiles), then the
     library GEMM multiplies it with the bias in its epilogue.  N / 16 not a
@@ -395,8 +395,8 @@ def test_library_gemm_size_class_reuses_timed_choice(mode):
                          ids=["non_monotone", "skip_all", "all_planes", "tied", "quantiles"])
 @pytest.mark.parametrize("M,K,N", [(512, 1056, 512), (300, 96, 22016)])
 def test_prefill_library_gemm_graded(M, K, N, t, max_bits, dtype):
-    """Graded (union) batches of 512 rows, and of 257-511 rows when the fused
-    grid would need more than one round (300 x 22016): the dequant kernel writes
+    """Graded (union) batches of 512 rows, and of 257-511 rows when K <= 8192
+    or the fused grid would need more than one round (300 x 22016): the dequant kernel writes
     RNE(w_eff * s) from each row's zone set (inactive planes masked to zero,
     midpoint bias added), then the library GEMM.  Zone sets that are not
     prefixes, none, all, tied thresholds and the 70/20/8/2 % quantile mix, held

@@ -93,7 +93,7 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow
   w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
   w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
   w.library_gemm = allow_library && M > kDecodeMaxRows &&
-                   (use_library_gemm(M, N, GRINQH_DTYPE_F16) || use_library_gemm(M, N, GRINQH_DTYPE_BF16));
+                   (use_library_gemm(M, K, N, GRINQH_DTYPE_F16) || use_library_gemm(M, K, N, GRINQH_DTYPE_BF16));
   if (w.library_gemm) {
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.chunk_off = round_up(w.partial_off + partial, 256);
@@ -135,7 +135,7 @@ bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64
 // reduce the union statistic over all M rows).
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
-  if (wl.library_gemm && use_library_gemm(M, d.N, dtype)) {  // the (graded) weight once, then the library GEMM
+  if (wl.library_gemm && use_library_gemm(M, d.K, d.N, dtype)) {  // the (graded) weight once, then the library GEMM
     // an error a library left in this thread's last-error slot must not be
     // taken for a failure of the launches below
     (void)hipGetLastError();

@@ -137,14 +137,18 @@ constexpr int64_t kLibraryGemmRowsBf16 = 224;
 // Whether a prefill product takes the library path.  Batches of 257-511 rows
 // take it too when the fused kernel's grid of 128-row tiles needs more than
 // one round of blocks (it is then not split over K, and each round runs the
-// whole K): gate_up at 320 rows took 213 us fused, 141 us here (graded at 384
-// rows: 259 against 161), while qkv, o_proj and down (at most 96 blocks)
-// stay within 15 us either way.
-inline bool use_library_gemm(int64_t M, int64_t N, int dtype) {
+// whole K: gate_up at 320 rows took 227 us fused, 143 us here), or when K is
+// at most kLibraryMaxKMidRows (qkv at 320 / 384 / 448 rows: 55 / 57 / 72 us
+// fused, 52 / 52 / 52 here, graded 68 / 70 / 89 against 57 / 60 / 62; o_proj
+// 2-16 % faster here).  down (K = 14336) stays fused there (dense 95 / 98 /
+// 116 us against 105 / 108 / 121); up to 256 rows the fused kernel is faster
+// (qkv at 256 rows: 42 against 58 us).
+constexpr int64_t kLibraryMaxKMidRows = 8192;
+inline bool use_library_gemm(int64_t M, int64_t K, int64_t N, int dtype) {
   if (N % 64 != 0) return false;
   if (M >= kLibraryGemmRows) return true;
   if (dtype == GRINQH_DTYPE_BF16 && M >= kLibraryGemmRowsBf16) return true;
-  return M > 256 && ((N / 16 + 15) / 16) * ((M + 127) / 128) > kTargetBlocks;
+  return M > 256 && (K <= kLibraryMaxKMidRows || ((N / 16 + 15) / 16) * ((M + 127) / 128) > kTargetBlocks);
 }
 // Graded fp16 library path: the dense weight RNE(w_eff * s) overflows fp16
 // where |w_eff| * |s| > 65504, which the reference's union GEMV (fp32
