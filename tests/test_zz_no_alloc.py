@@ -6,9 +6,10 @@ time with a smaller batch (the scratch array keeps the first call's contents:
 counters must be back at zero, partial sums must not leak), and checks both
 results bitwise against grinqh_gemm_or_gemv on the same inputs: the GEMV
 (one and four rows), the decode kernel (graded and dense), the fused prefill
-(graded, dense, and split over K).  From 512 rows the workspace entry point
-takes the library GEMM while the allocation-free one keeps the fused kernel,
-so that case is held to the oracle instead.
+(graded, dense, and split over K).  From 512 rows (and from 257 with
+K <= 8192) the workspace entry point takes the library GEMM while the
+allocation-free one keeps the fused kernels, so that case is held to the
+oracle instead.
 """
 import ctypes
 
@@ -62,7 +63,7 @@ CASES = [
     (4096, 28672, "union", 4, 2),         # four-row GEMV, in-kernel split-K completion
     (4096, 6144, "union", 64, 20),        # decode, batch statistic, scaled path
     (4096, 4096, "dense", 16, 5),         # decode, one m-tile
-    (1024, 2048, "dense", 300, 100),      # fused prefill
+    (1024, 2048, "dense", 250, 100),      # fused prefill
     (512, 1024, "union", 200, 80),        # graded fused prefill
     (2080, 256, "dense", 100, 70),        # fused prefill split over K (partial sums)
 ]
