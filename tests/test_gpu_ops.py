@@ -591,6 +591,32 @@ def test_decode_short_k_ranges(K, M, dtype):
     assert_output_close(y, own, O.bias_add(own, None, dtype), dtype, what=f"K={K} M={M}")
 
 
+@pytest.mark.parametrize("max_bits", BITS)
+@pytest.mark.parametrize("gs", [32, 64, 96, 256])
+@pytest.mark.parametrize("M,K", [(33, 3072), (64, 1184), (48, 4096)])
+def test_decode_64_row_group_sizes(M, K, gs, max_bits):
+    """33-64 rows in fp16 (the scaled path, which stages the scales of up to
+    65 groups per block) at every bit width and group sizes of 1-8 tiles.
+    K = 1184 is 37 tiles, so the waves' tile counts are odd and even, and the
+    last group is partial for every group size; both grading modes."""
+    from grinqh.kernel import grinqh_gemv_batch_union, grinqh_prefill_dense
+    rng = np.random.default_rng(900 + M + K + gs + max_bits)
+    N, dtype = 512, "float16"
+    W = rand_weight(rng, K, N, max_bits)
+    x = to_dtype_np(rng.standard_normal((M, K)), dtype)
+    s = to_dtype_np(rng.standard_normal((math.ceil(K / gs), N)), dtype)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    P = _prepare(W, max_bits)
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), P, _tdt(s, dtype), _tdt(bias, dtype), max_bits, gs, N // 4, t)
+    own = own_product(x, W, s, t, max_bits, gs, dtype, graded=True)
+    assert_output_close(y, own, O.bias_add(own, bias, dtype), dtype, bias=bias, what=f"graded M={M} K={K} gs={gs}")
+    yd = grinqh_prefill_dense(_tdt(x, dtype), P, _tdt(s, dtype), gs, N // 4, max_bits)
+    own = own_product(x, W, s, None, max_bits, gs, dtype, graded=False)
+    assert_output_close(yd, own, O.bias_add(own, None, dtype), dtype, what=f"dense M={M} K={K} gs={gs}")
+
+
 @pytest.mark.parametrize("mode", ["union", "dense"])
 @pytest.mark.parametrize("M", [20, 40, 64, 130])
 def test_large_scales_round_once(M, mode):
