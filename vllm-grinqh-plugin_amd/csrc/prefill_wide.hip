@@ -138,17 +138,21 @@ __global__ __launch_bounds__(256, 1) void prefill_wide_kernel(PrefillParams p) {
   };
   // Loads: the stage moves the lane offset (one VALU add per family), the
   // scalar offsets are loop invariant.  x: lane row m0 + tid / 8, chunk
-  // tid % 8, piece i 32 rows further down; rows past M read past the buffer's
-  // end (prefill_wide_applies bounds (M + 256) * ldx * 2 below 2^31) and load 0.
+  // tid % 8, piece i 32 rows further down.  Rows past M must load 0, so the
+  // whole offset of an x piece goes in the vector offset, the part the
+  // buffer's range check certainly covers (the scalar offset is not relied
+  // on for it); prefill_wide_applies bounds (M + 256) * ldx * 2 below 2^31,
+  // so no offset wraps.
   const uint32_t x_lane_off = (uint32_t)(((int64_t)(m0 + (tid >> 3)) * p.ldx + 8 * (tid & 7)) * 2);
-  uint32_t x_soff[8];
+  uint32_t x_piece_off[8];  // wave-uniform
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x_soff[i] = (uint32_t)i * (uint32_t)(32 * p.ldx * 2);
+  for (int i = 0; i < 8; ++i) x_piece_off[i] = (uint32_t)i * (uint32_t)(32 * p.ldx * 2);
   auto load_x = [&](int s, Slot& S) {
     const uint32_t voff = x_lane_off + (uint32_t)(s * BK * 2);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      S.xa[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)voff, (int)x_soff[i], 0));
+      S.xa[i] = __builtin_bit_cast(
+          u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xr, (int)(voff + x_piece_off[i]), 0, 0));
   };
   // planes: lane rows 8*rg8.. of the stage, word column w0 + wcol; row e and
   // plane z by scalar offset
