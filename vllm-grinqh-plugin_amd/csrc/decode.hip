@@ -525,30 +525,43 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
         for (int b = 0; b < 4; ++b) Y[mt][jj][b] *= up;
   }
 
-  // ---- phase 3: reduce the K sub-ranges of this block in fixed order kw = 0, 1, ...,
-  // one m-tile per round (the staging area is free now and holds one slot per
-  // contributing wave)
+  // ---- phase 3: reduce the K sub-ranges of this block, one m-tile per round.
+  // The sums of m-tile mt are added by the waves of K sub-range mt % KW (its
+  // owner), in fixed order kw = 0, 1, ..., KW-1, and those waves write that
+  // m-tile's outputs, so that the block's stores are spread over its waves:
+  // at 64 rows each wave stores 32 values per lane instead of two waves
+  // storing 128, which is more agent-scope stores than one wave keeps in
+  // flight (it then waits for them to reach memory).  The other sub-ranges
+  // leave their sums in the staging area, free now, one slot per wave.
+  auto owns = [&](int mt) { return kw == mt % KW; };  // wave-uniform
   if (KW > 1) {
+    constexpr int SLOT = NJ * 4 * 64;  // f32x4 per wave slot
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      const int own = mt % KW;
       __syncthreads();
-      if (kw > 0) {
-        f32x4_t* slot = s_red + ((kw - 1) * JG + jg) * NJ * 4 * 64;
+      if (kw != own) {
+        f32x4_t* slot = s_red + ((kw < own ? kw : kw - 1) * JG + jg) * SLOT;
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
           for (int b = 0; b < 4; ++b) slot[(jj * 4 + b) * 64 + lane] = Y[mt][jj][b];
       }
       __syncthreads();
-      if (kw == 0) {
+      if (kw == own) {
 #pragma unroll
-        for (int k2 = 1; k2 < KW; ++k2) {
-          const f32x4_t* slot = s_red + ((k2 - 1) * JG + jg) * NJ * 4 * 64;
+        for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-          for (int jj = 0; jj < NJ; ++jj)
+          for (int b = 0; b < 4; ++b) {
+            auto part = [&](int k2) -> f32x4_t {  // sub-range k2's sums
+              if (k2 == own) return Y[mt][jj][b];
+              return s_red[((k2 < own ? k2 : k2 - 1) * JG + jg) * SLOT + (jj * 4 + b) * 64 + lane];
+            };
+            f32x4_t acc = part(0);
 #pragma unroll
-            for (int b = 0; b < 4; ++b) Y[mt][jj][b] += slot[(jj * 4 + b) * 64 + lane];
-        }
+            for (int k2 = 1; k2 < KW; ++k2) acc += part(k2);
+            Y[mt][jj][b] = acc;
+          }
       }
     }
   }
@@ -557,22 +570,25 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // non-finite activation become NaN, as in the reference
   if constexpr (SC && !DENSE) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!owns(mt)) continue;
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
           for (int e = 0; e < 4; ++e) Y[mt][jj][b][e] = graded_nonfinite_to_nan(Y[mt][jj][b][e]);
+    }
   }
 
   // ---- phase 4: output (direct, or split-K partials + last-block reduction)
   // Output (m, n) of this lane: m = 16*mt + 4*q + e, n = (4*(jg*NJ+jj)+b)*NW + w0 + c.
   auto col_of = [&](int jj, int b) -> int64_t { return (int64_t)(4 * (jg * NJ + jj) + b) * p.NW + wc; };
   if (p.splits == 1) {
-    if (kw == 0 && col_ok) {
+    if (col_ok) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt) {
+        if (!owns(mt)) continue;
 #pragma unroll
         for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
@@ -583,17 +599,50 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
               if (m < p.M) p.y[(int64_t)m * p.N + col_of(jj, b)] = finish_output<DT>(Y[mt][jj][b][e], p.bias,
                                                                                   (int)col_of(jj, b));
             }
+      }
     }
     return;
   }
 
   // Split-K: this K range's partial sums go to partial[split][m][n]; the
   // range that finishes last (or the reduce kernel that follows on the
-  // stream) adds the ranges in fixed order.
-  if (kw == 0 && col_ok) {
+  // stream) adds the ranges in fixed order.  Agent-scope (sc1) stores: the
+  // last range may read them from another XCD, and before the reduce kernel
+  // they stream out during the kernel instead of being written back from L2
+  // at its end.  With a slab of partial sums below 2 GiB they are raw buffer
+  // stores without branches: the row part of an offset (past the slab for
+  // rows m >= M and lanes past the last word column, whose stores the range
+  // check drops) in the vector offset, the column tile's part in the scalar
+  // offset.
+  if ((int64_t)p.M * p.N * 4 < ((int64_t)1 << 31)) {
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(p.partial + (int64_t)split * p.M * p.N, (short)0,
+                                          (int)((uint32_t)p.M * (uint32_t)p.N * 4u), 0x00020000);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!owns(mt)) continue;
+      uint32_t roff[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = 16 * mt + 4 * q + e;
+        roff[e] = (m < p.M && col_ok) ? ((uint32_t)m * (uint32_t)p.N + (uint32_t)wc) * 4u : 0x80000000u;
+      }
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t coff = (uint32_t)(4 * (jg * NJ + jj) + b) * (uint32_t)p.NW * 4u;  // wave-uniform
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Y[mt][jj][b][e]), prs, (int)roff[e], (int)coff,
+                                                  kCpolSc1);
+        }
+    }
+  } else if (col_ok) {
     float* part = p.partial + (int64_t)split * p.M * p.N;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      if (!owns(mt)) continue;
 #pragma unroll
       for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
@@ -603,6 +652,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
             const int m = 16 * mt + 4 * q + e;
             if (m < p.M) store_partial(&part[(int64_t)m * p.N + col_of(jj, b)], Y[mt][jj][b][e]);
           }
+    }
   }
   if (p.counters != nullptr) splitk_complete<DT, 4 * MT * 256 / NT, NT>(p, lb % col_blocks, w0, 16);
 }
