@@ -67,7 +67,7 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
   constexpr int XS = RMAX + 8;                 // halves per staged x row
   constexpr int X_BYTES = 5 * XS * 2;          // x rows 0..3, row 4 all zero
   constexpr int OFF_BYTES = RMAX * Z * 4;
-  constexpr int RED_BYTES = 3 * 16 * MR * 64 * 4;  // partial sums of waves 1..3
+  constexpr int RED_BYTES = 3 * 16 * MR * 64 * 4;  // each dword's sums of the three waves not owning it
   constexpr int POOL_BYTES = (X_BYTES + OFF_BYTES) > RED_BYTES ? (X_BYTES + OFF_BYTES) : RED_BYTES;
   constexpr int SCG = kGemvScaleGroups;
   constexpr int CPR = RMAX / 8;                // 16-byte chunks per staged x row
@@ -306,43 +306,77 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     if (t + 1 < t_end) step(t + 1, DB, false, DC);
   }
 
-  // ---- phase 3: add the waves' sub-ranges in order 0, 1, 2, 3
+  // ---- phase 3: add the waves' sub-ranges in order 0, 1, 2, 3.  Wave j owns
+  // output dword j (columns (4j + b) * NW + w): it adds that dword's sums of
+  // all four waves and writes its outputs, so that the block's stores are
+  // spread over its waves (at four rows 16 per lane each, instead of 64 for
+  // wave 0).  Slot (j, k') holds the sums of the k'-th other wave.
   __syncthreads();
-  if (wave > 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 4; ++j) {
+    if (wave == j) continue;
+    const int k1 = wave < j ? wave : wave - 1;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int i = 0; i < MR; ++i) s_red[((wave - 1) * 16 * MR + (4 * j + b) * MR + i) * 64 + lane] = Y[j][b][i];
+      for (int i = 0; i < MR; ++i) s_red[(((j * 3 + k1) * 4 + b) * MR + i) * 64 + lane] = Y[j][b][i];
   }
   __syncthreads();
-  if (wave == 0) {
-#pragma unroll 1
-    for (int k = 0; k < 3; ++k)
+  float O[4][MR];  // this wave's dword: the block's sums
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 4; ++j) {
+    if (wave != j) continue;
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-          for (int i = 0; i < MR; ++i) Y[j][b][i] += s_red[(k * 16 * MR + (4 * j + b) * MR + i) * 64 + lane];
+      for (int i = 0; i < MR; ++i) {
+        auto part = [&](int k) -> float {  // wave k's sum
+          if (k == j) return Y[j][b][i];
+          return s_red[(((j * 3 + (k < j ? k : k - 1)) * 4 + b) * MR + i) * 64 + lane];
+        };
+        float acc = part(0);
+#pragma unroll
+        for (int k = 1; k < 4; ++k) acc += part(k);
+        O[b][i] = acc;
+      }
+  }
 
-    // ---- phase 4: output column n = (4j + b) * NW + w of rows m < M
+  // ---- phase 4: output column n = (4 * wave + b) * NW + w of rows m < M
+  if (p.splits == 1) {
     if (col_ok) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int b = 0; b < 4; ++b) {
+        const int64_t n = (int64_t)(4 * wave + b) * p.NW + wc;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int64_t n = (int64_t)(4 * j + b) * p.NW + wc;
+        for (int i = 0; i < MR; ++i)
+          if (i < p.M) p.y[(int64_t)i * p.N + n] = finish_output<DT>(O[b][i], p.bias, (int)n);
+      }
+    }
+  } else if ((int64_t)p.M * p.N * 4 < ((int64_t)1 << 31)) {
+    // agent-scope (sc1) raw buffer stores without branches: rows m >= M and
+    // lanes past the last word column get an offset past the K range's slab
+    // (dropped by the range check); the column tile's part is the scalar offset
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(p.partial + (int64_t)split * p.M * p.N, (short)0,
+                                          (int)((uint32_t)p.M * (uint32_t)p.N * 4u), 0x00020000);
+    uint32_t roff[MR];
 #pragma unroll
-          for (int i = 0; i < MR; ++i) {
-            if (i >= p.M) break;
-            if (p.splits == 1)
-              p.y[(int64_t)i * p.N + n] = finish_output<DT>(Y[j][b][i], p.bias, (int)n);
-            else
-              store_partial(&p.partial[((int64_t)split * p.M + i) * p.N + n], Y[j][b][i]);
-          }
-        }
+    for (int i = 0; i < MR; ++i)
+      roff[i] = (i < p.M && col_ok) ? ((uint32_t)i * (uint32_t)p.N + (uint32_t)wc) * 4u : 0x80000000u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t coff = (uint32_t)(4 * wave + b) * (uint32_t)p.NW * 4u;  // wave-uniform
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O[b][i]), prs, (int)roff[i], (int)coff, kCpolSc1);
+    }
+  } else if (col_ok) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int64_t n = (int64_t)(4 * wave + b) * p.NW + wc;
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+        if (i < p.M) store_partial(&p.partial[((int64_t)split * p.M + i) * p.N + n], O[b][i]);
     }
   }
   // the K range that finishes last adds all ranges' partial sums of this column block
