@@ -816,7 +816,7 @@ static void launch_reduce_dt(const DecodeParams& p, int splits, hipStream_t st) 
   // lanes per 4-column chunk: one lane adds up to 16 ranges with all its
   // loads in flight (qkv, o_proj and down at 16 and 64 rows: 3-6 % faster
   // products than four lanes and a butterfly); 64 ranges and more take 16
-  // lanes (four lanes of 16 loads each were 10-14 % slower there)
+  // lanes (four lanes of 16 loads each were 5-14 % slower there)
   if (splits >= 64)
     launch_reduce_t<DT, 16>(p, splits, st);
   else if (splits > 16)
