@@ -95,7 +95,7 @@ WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow
   w.library_gemm = allow_library && M > kDecodeMaxRows &&
                    (use_library_gemm(M, K, N, GRINQH_DTYPE_F16) || use_library_gemm(M, K, N, GRINQH_DTYPE_BF16));
   if (w.library_gemm) {
-    const int64_t chunks = sigma_chunk_count(M);
+    const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.chunk_off = round_up(w.partial_off + partial, 256);
     w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
     // graded: the overflow guard's scale-range slots, then the GEMM's alpha vector
@@ -140,10 +140,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     // taken for a failure of the launches below
     (void)hipGetLastError();
     uint16_t* wt = reinterpret_cast<uint16_t*>(ws + wl.wt_off);
-    // graded: the statistic pass's column maxima of row chunks (the
-    // dequantization reduces them for its rows)
-    float* chunk_max = graded ? reinterpret_cast<float*>(ws + wl.chunk_off) : nullptr;
-    const int chunks = sigma_chunk_count(M);
+    float* sigma = graded ? reinterpret_cast<float*>(ws + wl.sigma_off) : nullptr;
     uint8_t* flags = reinterpret_cast<uint8_t*>(ws + wl.flag_off);
     // graded fp16: the overflow guard of the dense weight (scale-range slots, alpha on the device)
     const bool guard = graded && dtype == GRINQH_DTYPE_F16;
@@ -152,13 +149,12 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
         guard ? reinterpret_cast<float*>(ws + wl.range_off + round_up((size_t)scale_range_slots(d.K) * 4, 256))
               : nullptr;
     const int64_t n_scale = (int64_t)((d.K + d.gs - 1) / d.gs) * d.N;
-    int rc = graded ? launch_sigma_chunks(xs, d.ldx, (int)M, d.K, dtype, chunk_max, flags,
-                                          guard ? d.scale : nullptr, n_scale, slots, st)
+    int rc = graded ? launch_sigma_chunks(xs, d.ldx, (int)M, d.K, dtype, reinterpret_cast<float*>(ws + wl.chunk_off),
+                                          flags, sigma, guard ? d.scale : nullptr, n_scale, slots, st)
                     : GRINQH_OK;
     if (rc != GRINQH_OK) return rc;
     auto dequant = [&](hipStream_t s) {
-      return launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, chunk_max, chunks, d.thr, slots,
-                               alpha, s);
+      return launch_dequant_nk(d.planes, d.scale, wt, d.K, d.N, d.gs, max_bits, dtype, sigma, d.thr, slots, alpha, s);
     };
     arm_kernel_timing();
     rc = dequant(st);

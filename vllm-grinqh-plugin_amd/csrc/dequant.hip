@@ -37,8 +37,7 @@ struct DequantParams {
   const uint32_t* planes;
   const uint16_t* scale;
   uint16_t* wt;        // [N][K]
-  const float* partial;  // graded: column maxima of the batch's row chunks [chunks][K]
-  int chunks;
+  const float* sigma;  // graded: union statistic [K]
   GradeThresholds thr;
   int K, N, NW, gs;
   const uint32_t* slots;  // graded fp16: scale-range slots (overflow guard), else nullptr
@@ -67,23 +66,6 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
     if (lane == 0) s_wmax[wave] = hm;
-  }
-  // graded: the union statistic of the block's 64 rows, the maximum of the
-  // statistic pass's chunk maxima (NaN ignored unless every one is NaN, as
-  // fmaxf does; exact in any order): a quarter of the chunks per wave, four
-  // loads in flight, combined per row at grading
-  __shared__ float s_sig[4][kDqRowsPerBlock];
-  if constexpr (!DENSE) {
-    const int r = threadIdx.x & 63, k = min(kb + r, p.K - 1);  // rows past K read a valid one, unused
-    float sm = __int_as_float(0x7fc00000);
-    for (int c0 = wave; c0 < p.chunks; c0 += 16) {
-      float v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = p.partial[(int64_t)min(c0 + 4 * j, p.chunks - 1) * p.K + k];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sm = fmaxf(sm, v[j]);
-    }
-    s_sig[wave][r] = sm;
   }
   {  // NW % 4 == 0: a 4-word piece is wholly inside or outside the row
     const int pc = threadIdx.x & 7;  // 4-word piece of the block's 32 columns
@@ -140,9 +122,7 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     if constexpr (!DENSE) {  // graded: inactive planes masked to zero
-      const int rr = k0 + e - kb;
-      const float sg = fmaxf(fmaxf(s_sig[0][rr], s_sig[1][rr]), fmaxf(s_sig[2][rr], s_sig[3][rr]));
-      const uint32_t bits = zone_bits<Z>(sg, p.thr.t);
+      const uint32_t bits = zone_bits<Z>(p.sigma[k0 + e], p.thr.t);
       beta[e] = midpoint_bias<Z>(bits);
 #pragma unroll
       for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((bits >> z) & 1u);
@@ -199,45 +179,12 @@ __global__ __launch_bounds__(256) void dequant_nk_kernel(DequantParams p) {
 // and writes its column maxima to partial[chunk][k] (NaN ignored unless every
 // value is NaN, as fmaxf does).  It also records, per row, whether the row's
 // 256 values hold an inf or NaN: flags[column block][m].
-//
-// With slots != nullptr, block b of the first chunk also writes slots[b] = the
-// largest |value| (fp16 bits) of its share of the n_scale scales (the
-// overflow guard of the graded fp16 dequantization).
 template <typename DT>
 __global__ __launch_bounds__(256) void sigma_chunks_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
                                                            int rows_per_chunk, float* __restrict__ partial,
-                                                           uint8_t* __restrict__ flags,
-                                                           const uint16_t* __restrict__ scale, int64_t n_scale,
-                                                           uint32_t* __restrict__ slots) {
+                                                           uint8_t* __restrict__ flags) {
   constexpr uint32_t EXP = DT::id == F16::id ? 0x7C00u : 0x7F80u;  // all-ones exponent: inf or NaN
   __shared__ float s_part[8][256 + 4];
-  __shared__ uint32_t s_smax[4];
-  if (slots != nullptr && blockIdx.y == 0) {
-    // this block's share of the scales (whole 16-byte vectors when the array
-    // is 16-byte aligned), four vectors per thread in flight
-    const int64_t per = ((n_scale + gridDim.x - 1) / gridDim.x + 7) & ~(int64_t)7;
-    const int64_t i0 = min((int64_t)blockIdx.x * per, n_scale), i1 = min(i0 + per, n_scale);
-    uint32_t hm = 0;
-    int64_t tail = i0;
-    if ((reinterpret_cast<uintptr_t>(scale) & 15u) == 0) {
-      const int64_t nv = (i1 - i0) / 8;
-      const u32x4_t* sv = reinterpret_cast<const u32x4_t*>(scale + i0);
-      for (int64_t j = threadIdx.x; j < nv; j += 4 * 256) {
-        u32x4_t v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = j + 256 * u < nv ? sv[j + 256 * u] : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) hm = max(hm, max(v[u][q] & 0x7FFFu, (v[u][q] >> 16) & 0x7FFFu));
-      }
-      tail = i0 + 8 * nv;
-    }
-    for (int64_t i = tail + threadIdx.x; i < i1; i += 256) hm = max(hm, (uint32_t)scale[i] & 0x7FFFu);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
-    if ((threadIdx.x & 63) == 0) s_smax[threadIdx.x >> 6] = hm;
-  }
   const int l = threadIdx.x & 31, g = threadIdx.x >> 5;
   const int k = blockIdx.x * 256 + 8 * l;
   const bool col_ok = k < K;  // K % 8 == 0: a lane's 8 columns are all in or all out
@@ -280,8 +227,64 @@ __global__ __launch_bounds__(256) void sigma_chunks_kernel(const uint16_t* __res
     for (int gg = 1; gg < 8; ++gg) r = fmaxf(r, s_part[gg][threadIdx.x]);
     partial[(int64_t)blockIdx.y * K + kk] = r;
   }
-  if (slots != nullptr && blockIdx.y == 0 && threadIdx.x == 0)
-    slots[blockIdx.x] = max(max(s_smax[0], s_smax[1]), max(s_smax[2], s_smax[3]));
+}
+
+// Second pass: sigma[k] = fmaxf over the chunks' maxima (exact in any order).
+// A block takes 64 columns; its 4 waves take every 4th chunk, 4 loads in
+// flight each, and combine through LDS.
+// With slots != nullptr, block b also writes slots[b] = the largest |value|
+// (fp16 bits) of its share of the n_scale scales (the overflow guard of the
+// graded fp16 dequantization).
+__global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* __restrict__ partial, int chunks,
+                                                                  int K, float* __restrict__ sigma,
+                                                                  const uint16_t* __restrict__ scale,
+                                                                  int64_t n_scale, uint32_t* __restrict__ slots) {
+  __shared__ float s_part[4][64];
+  __shared__ uint32_t s_smax[4];
+  const int cl = threadIdx.x & 63, cg = threadIdx.x >> 6;
+  if (slots != nullptr) {
+    // each block's share of the scales (whole 16-byte vectors when the
+    // array is 16-byte aligned), four vectors per thread in flight
+    const int64_t per = ((n_scale + gridDim.x - 1) / gridDim.x + 7) & ~(int64_t)7;
+    const int64_t i0 = min((int64_t)blockIdx.x * per, n_scale), i1 = min(i0 + per, n_scale);
+    uint32_t hm = 0;
+    int64_t tail = i0;
+    if ((reinterpret_cast<uintptr_t>(scale) & 15u) == 0) {
+      const int64_t nv = (i1 - i0) / 8;
+      const u32x4_t* sv = reinterpret_cast<const u32x4_t*>(scale + i0);
+      for (int64_t j = threadIdx.x; j < nv; j += 4 * 256) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = j + 256 * u < nv ? sv[j + 256 * u] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) hm = max(hm, max(v[u][q] & 0x7FFFu, (v[u][q] >> 16) & 0x7FFFu));
+      }
+      tail = i0 + 8 * nv;
+    }
+    for (int64_t i = tail + threadIdx.x; i < i1; i += 256) hm = max(hm, (uint32_t)scale[i] & 0x7FFFu);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
+    if (cl == 0) s_smax[cg] = hm;
+  }
+  const int k = blockIdx.x * 64 + cl;
+  const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
+  float s = __int_as_float(0x7fc00000);
+  for (int c0 = cg; c0 < chunks; c0 += 16) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = min(c0 + 4 * j, chunks - 1);  // past the end: repeats the last chunk
+      v[j] = partial[(int64_t)c * K + kc];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s = fmaxf(s, v[j]);
+  }
+  s_part[cg][cl] = s;
+  __syncthreads();
+  if (cg == 0 && k < K) sigma[k] = fmaxf(fmaxf(s_part[0][cl], s_part[1][cl]), fmaxf(s_part[2][cl], s_part[3][cl]));
+  if (slots != nullptr && threadIdx.x == 0) slots[blockIdx.x] = max(max(s_smax[0], s_smax[1]), max(s_smax[2], s_smax[3]));
 }
 
 // Graded products: a row of x holding a non-finite value has every output
@@ -316,29 +319,27 @@ int launch_dequant_dt(const DequantParams& p, int max_bits, hipStream_t st) {
 }  // namespace
 
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
-                      int max_bits, int dtype, const float* partial, int chunks, const GradeThresholds& thr,
+                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr,
                       const uint32_t* slots, float* alpha, hipStream_t st) {
   if (K % 32 != 0 || N % 64 != 0 || gs % 32 != 0 || (int64_t)K * N >= ((int64_t)1 << 40)) return GRINQH_ERR_INVALID;
-  if (partial != nullptr && chunks < 1) return GRINQH_ERR_INVALID;
-  const DequantParams p{planes, scale, wt, partial, chunks, thr, K, N, N / 16, gs, slots, scale_range_slots(K), alpha};
+  const DequantParams p{planes, scale, wt, sigma, thr, K, N, N / 16, gs, slots, scale_range_slots(K), alpha};
   const bool bf16 = dtype == GRINQH_DTYPE_BF16;
-  if (partial == nullptr)
+  if (sigma == nullptr)
     return bf16 ? launch_dequant_dt<BF16, true>(p, max_bits, st) : launch_dequant_dt<F16, true>(p, max_bits, st);
   return bf16 ? launch_dequant_dt<BF16, false>(p, max_bits, st) : launch_dequant_dt<F16, false>(p, max_bits, st);
 }
 
 int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
-                        const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st) {
+                        float* sigma, const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st) {
   if (M <= 0 || K <= 0 || K % 8 != 0) return GRINQH_ERR_INVALID;
-  const int rows = sigma_chunk_rows(M), chunks = sigma_chunk_count(M);
-  const dim3 grid((unsigned)((K + 255) / 256), (unsigned)chunks);  // grid.x == scale_range_slots(K)
-  uint32_t* sl = scale != nullptr ? slots : nullptr;
+  const int rows = sigma_chunk_rows(M), chunks = (M + rows - 1) / rows;
+  const dim3 grid((unsigned)((K + 255) / 256), (unsigned)chunks);
   if (dtype == GRINQH_DTYPE_BF16)
-    hipLaunchKernelGGL(sigma_chunks_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags, scale,
-                       n_scale, sl);
+    hipLaunchKernelGGL(sigma_chunks_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
   else
-    hipLaunchKernelGGL(sigma_chunks_kernel<F16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags, scale,
-                       n_scale, sl);
+    hipLaunchKernelGGL(sigma_chunks_kernel<F16>, grid, dim3(256), 0, st, x, ldx, M, K, rows, partial, flags);
+  hipLaunchKernelGGL(sigma_chunks_reduce_kernel, dim3((unsigned)scale_range_slots(K)), dim3(256), 0, st, partial,
+                     chunks, K, sigma, scale, n_scale, scale != nullptr ? slots : nullptr);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

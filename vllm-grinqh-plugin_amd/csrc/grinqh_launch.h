@@ -153,33 +153,30 @@ inline bool use_library_gemm(int64_t M, int64_t K, int64_t N, int dtype) {
 // Graded fp16 library path: the dense weight RNE(w_eff * s) overflows fp16
 // where |w_eff| * |s| > 65504, which the reference's union GEMV (fp32
 // products) does not.  The statistic pass also writes, per block of its
-// first row chunk, the largest |scale| (fp16 bits) of a share of the scale
-// array (scale_range_slots(K) words); the dequantization takes from them an
+// second pass, the largest |scale| (fp16 bits) of a share of the scale array
+// (scale_range_slots(K) words); the dequantization takes from them an
 // exponent e >= 0 that brings every |w_eff * s * 2^-e| within range, writes
 // RNE(w_eff * s * 2^-e) and fills the GEMM's alpha vector (one value per
 // output column, read from device memory) with 2^e.  e = 0 (alpha 1) for any
 // weight whose scales are below 65504 / 2^(max_bits-1).
-inline int scale_range_slots(int64_t K) { return (int)((K + 255) / 256); }
-// partial == nullptr: dense; else graded with the union statistic given as
-// the statistic pass's column maxima of `chunks` row chunks (chunks x K
-// floats), which each block reduces for its own rows.  slots / alpha (N
-// floats): the graded fp16 overflow guard (nullptr: none).
+inline int scale_range_slots(int64_t K) { return (int)((K + 63) / 64); }
+// sigma == nullptr: dense; else graded with the union statistic sigma[K].
+// slots / alpha (N floats): the graded fp16 overflow guard (nullptr: none).
 int launch_dequant_nk(const uint32_t* planes, const uint16_t* scale, uint16_t* wt, int K, int N, int gs,
-                      int max_bits, int dtype, const float* partial, int chunks, const GradeThresholds& thr,
+                      int max_bits, int dtype, const float* sigma, const GradeThresholds& thr,
                       const uint32_t* slots, float* alpha, hipStream_t st);
-// Union statistic of a graded library-path batch: column maxima of row
-// chunks (partial: chunks x K floats; their maximum is the statistic, taken
-// by the dequantization); flags (ceil(K/256) x M bytes) marks the rows
-// holding an inf or NaN.  Chunks of at least 32 rows, at most 64 chunks.
+// Union statistic of a graded library-path batch in two passes: column
+// maxima of row chunks (partial: chunks x K floats), then their maximum
+// (sigma: K floats); flags (ceil(K/256) x M bytes) marks the rows holding an
+// inf or NaN.  Chunks of at least 32 rows, at most 64 chunks.
 inline int sigma_chunk_rows(int64_t M) {
   const int64_t r = ((M + 63) / 64 + 7) / 8 * 8;
   return (int)(r > 32 ? r : 32);
 }
-inline int sigma_chunk_count(int64_t M) { return (int)((M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M)); }
 // scale != nullptr: also the scale-range slots of the overflow guard over the
 // n_scale values of scale
 int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
-                        const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st);
+                        float* sigma, const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st);
 // after the GEMM: the outputs of every flagged row become NaN
 int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st);
 // y[m][n] = alpha[n] * (x[M][K] @ wt[N][K]^T)[m][n] (+ bias[n]) in the
