@@ -617,6 +617,31 @@ def test_decode_64_row_group_sizes(M, K, gs, max_bits):
     assert_output_close(yd, own, O.bias_add(own, None, dtype), dtype, what=f"dense M={M} K={K} gs={gs}")
 
 
+@pytest.mark.parametrize("N", [400, 6160])
+@pytest.mark.parametrize("M", [1, 4, 16, 40, 64])
+def test_partial_column_blocks(M, N):
+    """Word-column counts that leave the last column block partial (25 and 385
+    plane-word columns: lanes past the last column hold a clamped copy whose
+    outputs and split-K partial sums must be dropped), through the split-K
+    path of the GEMV and decode kernels, graded with bias and dense."""
+    from grinqh.kernel import grinqh_gemv_batch_union, grinqh_prefill_dense
+    rng = np.random.default_rng(1300 + M + N)
+    K, b, gs, dtype = 2048, 8, 128, "float16"
+    W = rand_weight(rng, K, N, b)
+    x = to_dtype_np(rng.standard_normal((M, K)), dtype)
+    s = to_dtype_np(rng.standard_normal((K // gs, N)) * 0.05, dtype)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    P = _prepare(W, b)
+    y = grinqh_gemv_batch_union(_tdt(x, dtype), P, _tdt(s, dtype), _tdt(bias, dtype), b, gs, N // 4, t)
+    own = own_product(x, W, s, t, b, gs, dtype, graded=True)
+    assert_output_close(y, own, O.bias_add(own, bias, dtype), dtype, bias=bias, what=f"graded M={M} N={N}")
+    yd = grinqh_prefill_dense(_tdt(x, dtype), P, _tdt(s, dtype), gs, N // 4, b)
+    own = own_product(x, W, s, None, b, gs, dtype, graded=False)
+    assert_output_close(yd, own, O.bias_add(own, None, dtype), dtype, what=f"dense M={M} N={N}")
+
+
 @pytest.mark.parametrize("mode", ["union", "dense"])
 @pytest.mark.parametrize("M", [20, 40, 64, 130])
 def test_large_scales_round_once(M, mode):
