@@ -41,8 +41,9 @@
 //
 // Split-K partials are reduced deterministically: the K sub-ranges of a block
 // through LDS in fixed order; the K ranges of the grid either by the range
-// that finishes last (small reductions) or by a second kernel, both adding the
-// fp32 partials in range order before the output cast and bias.
+// that finishes last (small reductions: in range order) or by a second kernel
+// (in strided lane sums joined by a fixed butterfly), both in fp32 before the
+// output cast and bias, in an order that does not depend on timing.
 #include "grinqh_common.h"
 #include "grinqh_launch.h"
 #include "splitk_complete.h"
