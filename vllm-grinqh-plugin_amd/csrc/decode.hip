@@ -56,9 +56,9 @@ constexpr int kDecodeRowsPerBlock = 2048;  // rows per block at MT = 1 (x staged
 // built in registers as the prefill builds it in LDS, and accumulate the
 // output directly: no per-group partial sums, no correction column, no group
 // epilogue.  The registers this frees let a wave cover two output dwords of all
-// 64 rows (128 sums per lane), so the four waves are two output-dword pairs x
-// two K sub-ranges: each plane word and x element is loaded and unpacked by two
-// waves instead of four.  The weight is rounded once to fp16, as in the
+// 64 rows (128 sums per lane), so the eight waves are two output-dword pairs x
+// four K sub-ranges: each plane word and x element is loaded and unpacked by
+// two waves (one per dword pair) instead of four.  The weight is rounded once to fp16, as in the
 // reference's dense path (grinqh/kernel.py:586).
 template <typename DT, int MT>
 constexpr bool decode_scaled() { return MT >= 2 && DT::id == F16::id; }
