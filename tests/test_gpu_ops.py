@@ -469,6 +469,30 @@ def test_prefill_library_gemm_70b_qkv_shape(mode):
                         what=f"70B qkv M={M} {mode}")
 
 
+def test_prefill_without_library_algorithm_takes_fused_kernel():
+    """A product of 512 rows for which the library offers no GEMM algorithm
+    without workspace (K = 1048832, N = 64) takes the fused prefill kernel
+    instead of failing, graded (union statistic of all 512 rows) and dense.
+    The first 16 output rows are held to the oracle: S10 with the scaled
+    weight rounded to fp16, and S9."""
+    from grinqh.kernel import run_product
+    M, K, N, b, R = 512, 4097 * 256, 64, 8, 16
+    rng = np.random.default_rng(4097)
+    W = rand_weight(rng, K, N, b)
+    s = to_dtype_np(rng.standard_normal((K // 128, N)) * 0.05, "float16")
+    x = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
+    sigma = np.abs(x).max(0).astype(np.float64)  # no NaN in x: the union statistic
+    t = [0.0] + np.quantile(sigma, [0.7, 0.9, 0.98]).tolist()
+    P, st, xt = _prepare(W, b), _tdt(s, "float16"), torch.from_numpy(x).cuda()
+    xs = x[:R].astype(np.float64)
+    y = run_product(xt, P, st, None, b, 128, N // 4, t, "union")
+    pre = xs @ O.graded_weight_rounded(W, O.grade(sigma, t, b), s, b, 128, "float16")
+    assert_output_close(y[:R], pre, O.bias_add(pre, None, "float16"), "float16", what=f"graded K={K}")
+    y = run_product(xt, P, st, None, b, 128, N // 4, [0.0] * 4, "dense")
+    assert_output_close(y[:R], O.dense_prefill_f64(x[:R], W, s, 128, "float16"),
+                        O.dense_prefill(x[:R], W, s, None, 128, "float16"), "float16", what=f"dense K={K}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_prefill_library_gemm_strided_rows(dtype):
     """Library-GEMM prefill of activation rows with a leading dimension above

@@ -165,16 +165,9 @@ int fastest_candidate(const GemmPlan& pl, const hipblasLtMatmulAlgo_t* algos, in
   return ok ? best : 0;
 }
 
-// Builds the descriptors of one shape and takes, among the heuristic's
-// candidates that need no workspace, the fastest on the creating call's
-// operands (the heuristic's first choice ran the Llama-3-8B qkv, o_proj and
-// down GEMMs at 0.9-1.1 PFLOP/s against 1.3 for gate_up).  The heuristic does
-// not always honour the workspace limit of the preference (Llama-3-70B qkv at
-// 4096 rows: its first choice asked for 57 MiB of 32), so candidates that ask
-// for workspace are dropped.  While the caller's stream is being captured
-// into a graph no candidate is run: the heuristic's first is taken (warm-up
-// calls before the capture create the plans that are timed).
-bool make_plan(const GemmShape& s, GemmPlan& pl, const GemmCall& call) {
+// The descriptors of one shape (bias_ptr: the bias epilogue's pointer, or
+// nullptr when the shape has none).
+bool build_descriptors(const GemmShape& s, GemmPlan& pl, const void* bias_ptr) {
   const hipDataType dt = s.dtype == GRINQH_DTYPE_BF16 ? HIP_R_16BF : HIP_R_16F;
   pl.shape = s;
   if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
@@ -198,35 +191,66 @@ bool make_plan(const GemmShape& s, GemmPlan& pl, const GemmCall& call) {
             HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bdt, sizeof(bdt)) !=
             HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &call.bias,
-                                        sizeof(call.bias)) != HIPBLAS_STATUS_SUCCESS)
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias_ptr,
+                                        sizeof(bias_ptr)) != HIPBLAS_STATUS_SUCCESS)
       return blas_failed("bias epilogue attributes", -1, s);
   }
   if (hipblasLtMatrixLayoutCreate(&pl.a, dt, (uint64_t)s.K, (uint64_t)s.N, s.K) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&pl.b, dt, (uint64_t)s.K, (uint64_t)s.M, s.ldx) != HIPBLAS_STATUS_SUCCESS ||
       hipblasLtMatrixLayoutCreate(&pl.d, dt, (uint64_t)s.N, (uint64_t)s.M, s.N) != HIPBLAS_STATUS_SUCCESS)
     return blas_failed("matrix layout", -1, s);
+  return true;
+}
+
+constexpr int kCandidates = 16;
+
+// The heuristic's candidates for a described shape that need no workspace,
+// in its order of preference: their count (0 if it offered none), or -1 if
+// the query failed.  The heuristic does not always honour the workspace limit
+// of the preference (Llama-3-70B qkv at 4096 rows: its first choice asked for
+// 57 MiB of 32), so candidates that ask for workspace are dropped.
+int workspace_free_candidates(const GemmPlan& pl, hipblasLtMatmulAlgo_t* algos) {
+  const GemmShape& s = pl.shape;
   hipblasLtMatmulPreference_t pref = nullptr;
-  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return blas_failed("preference", -1, s);
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) {
+    blas_failed("preference", -1, s);
+    return -1;
+  }
   const uint64_t ws = 0;
   if (hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) !=
       HIPBLAS_STATUS_SUCCESS) {
     hipblasLtMatmulPreferenceDestroy(pref);
-    return blas_failed("workspace preference", -1, s);
+    blas_failed("workspace preference", -1, s);
+    return -1;
   }
-  constexpr int kCandidates = 16;
-  constexpr int kTimedCandidates = 8;
   hipblasLtMatmulHeuristicResult_t res[kCandidates];
   int found = 0;
   const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(handle_for_device(s.dev), pl.desc, pl.a, pl.b, pl.d,
                                                              pl.d, pref, kCandidates, res, &found);
   hipblasLtMatmulPreferenceDestroy(pref);
-  if (st != HIPBLAS_STATUS_SUCCESS || found < 1)
-    return blas_failed("heuristic", st == HIPBLAS_STATUS_SUCCESS ? -2 : (int)st, s);
-  hipblasLtMatmulAlgo_t algos[kCandidates];
+  if (st != HIPBLAS_STATUS_SUCCESS) {
+    blas_failed("heuristic", (int)st, s);
+    return -1;
+  }
   int n = 0;
   for (int i = 0; i < found && i < kCandidates; ++i)
     if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0) algos[n++] = res[i].algo;
+  return n;
+}
+
+// Builds the descriptors of one shape and takes, among the heuristic's
+// candidates that need no workspace, the fastest on the creating call's
+// operands (the heuristic's first choice ran the Llama-3-8B qkv, o_proj and
+// down GEMMs at 0.9-1.1 PFLOP/s against 1.3 for gate_up).  While the caller's
+// stream is being captured into a graph no candidate is run: the heuristic's
+// first is taken (warm-up calls before the capture create the plans that are
+// timed).
+bool make_plan(const GemmShape& s, GemmPlan& pl, const GemmCall& call) {
+  if (!build_descriptors(s, pl, call.bias)) return false;
+  constexpr int kTimedCandidates = 8;
+  hipblasLtMatmulAlgo_t algos[kCandidates];
+  const int n = workspace_free_candidates(pl, algos);
+  if (n < 0) return false;
   if (n == 0) return blas_failed("heuristic (no candidate without workspace)", -3, s);
   // The timed choice is kept per size class: M rounded up to a power of two
   // (with N, K, dtype and epilogue).  Another M of the class takes the same
@@ -264,6 +288,24 @@ void destroy_plan(GemmPlan& pl) {
 }
 
 }  // namespace
+
+bool gemm_x_wt_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int dtype, bool bias, bool alpha_vector) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  if (handle_for_device(dev) == nullptr) return false;
+  const GemmShape key{dev, M, N, K, ldx, dtype, bias, alpha_vector};
+  thread_local std::vector<std::pair<GemmShape, bool>> known;
+  for (const auto& e : known)
+    if (e.first == key) return e.second;
+  GemmPlan pl{};
+  // the bias pointer is an attribute the heuristic does not dereference
+  const void* dummy_bias = bias ? reinterpret_cast<const void*>(static_cast<uintptr_t>(256)) : nullptr;
+  hipblasLtMatmulAlgo_t algos[kCandidates];
+  const bool ok = build_descriptors(key, pl, dummy_bias) && workspace_free_candidates(pl, algos) > 0;
+  destroy_plan(pl);
+  known.emplace_back(key, ok);
+  return ok;
+}
 
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
               int64_t N, int64_t K, int dtype, const float* alpha_vec, hipStream_t st, const GemmPrelude* prelude) {

@@ -129,13 +129,17 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // larger activations.
 bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64_t)1 << 31); }
 
-// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm), else one
-// prefill launch over the whole batch, the wide-tile kernel where it applies
+// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm, when the
+// library has an algorithm without workspace for the shape), else one prefill
+// launch over the whole batch, the wide-tile kernel where it applies
 // (prefill_wide_applies) or the fused prefill kernel (graded batches first
-// reduce the union statistic over all M rows).
+// reduce the union statistic over all M rows).  The workspace layout holds
+// the fused kernel's regions in front of the library path's, so either runs.
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
-  if (wl.library_gemm && use_library_gemm(M, d.K, d.N, dtype)) {  // the (graded) weight once, then the library GEMM
+  if (wl.library_gemm && use_library_gemm(M, d.K, d.N, dtype) &&
+      gemm_x_wt_supported(M, d.N, d.K, d.ldx, dtype, d.bias != nullptr,
+                          graded && dtype == GRINQH_DTYPE_F16)) {  // the (graded) weight once, then the library GEMM
     // an error a library left in this thread's last-error slot must not be
     // taken for a failure of the launches below
     (void)hipGetLastError();
