@@ -230,21 +230,30 @@ __global__ __launch_bounds__(256) void sigma_chunks_kernel(const uint16_t* __res
 }
 
 // Second pass: sigma[k] = fmaxf over the chunks' maxima (exact in any order).
-// A block takes 64 columns; its 4 waves take every 4th chunk, 4 loads in
-// flight each, and combine through LDS.
+// A block takes 64 columns; its 4 waves take every 4th chunk, all of a wave's
+// loads (16 for the at most 64 chunks) in flight at once, and combine through
+// LDS.
 // With slots != nullptr, block b also writes slots[b] = the largest |value|
 // (fp16 bits) of its share of the n_scale scales (the overflow guard of the
-// graded fp16 dequantization).
+// graded fp16 dequantization), scanned while the chunk loads are in flight.
 __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* __restrict__ partial, int chunks,
                                                                   int K, float* __restrict__ sigma,
                                                                   const uint16_t* __restrict__ scale,
                                                                   int64_t n_scale, uint32_t* __restrict__ slots) {
+  constexpr int BATCH = 16;
   __shared__ float s_part[4][64];
   __shared__ uint32_t s_smax[4];
   const int cl = threadIdx.x & 63, cg = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + cl;
+  const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
+  // every load is issued (chunks past the end repeat the last one, which the
+  // maximum absorbs): a load under a condition was waited for at once
+  float v[BATCH];
+#pragma unroll
+  for (int j = 0; j < BATCH; ++j) v[j] = partial[(int64_t)min(cg + 4 * j, chunks - 1) * K + kc];
   if (slots != nullptr) {
     // each block's share of the scales (whole 16-byte vectors when the
-    // array is 16-byte aligned), four vectors per thread in flight
+    // array is 16-byte aligned), eight vectors per thread in flight
     const int64_t per = ((n_scale + gridDim.x - 1) / gridDim.x + 7) & ~(int64_t)7;
     const int64_t i0 = min((int64_t)blockIdx.x * per, n_scale), i1 = min(i0 + per, n_scale);
     uint32_t hm = 0;
@@ -252,14 +261,14 @@ __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* _
     if ((reinterpret_cast<uintptr_t>(scale) & 15u) == 0) {
       const int64_t nv = (i1 - i0) / 8;
       const u32x4_t* sv = reinterpret_cast<const u32x4_t*>(scale + i0);
-      for (int64_t j = threadIdx.x; j < nv; j += 4 * 256) {
-        u32x4_t v[4];
+      for (int64_t j = threadIdx.x; j < nv; j += 8 * 256) {
+        u32x4_t w[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = j + 256 * u < nv ? sv[j + 256 * u] : u32x4_t{0u, 0u, 0u, 0u};
+        for (int u = 0; u < 8; ++u) w[u] = j + 256 * u < nv ? sv[j + 256 * u] : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 8; ++u)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) hm = max(hm, max(v[u][q] & 0x7FFFu, (v[u][q] >> 16) & 0x7FFFu));
+          for (int q = 0; q < 4; ++q) hm = max(hm, max(w[u][q] & 0x7FFFu, (w[u][q] >> 16) & 0x7FFFu));
       }
       tail = i0 + 8 * nv;
     }
@@ -268,18 +277,14 @@ __global__ __launch_bounds__(256) void sigma_chunks_reduce_kernel(const float* _
     for (int o = 32; o >= 1; o >>= 1) hm = max(hm, (uint32_t)__shfl_xor((int)hm, o, 64));
     if (cl == 0) s_smax[cg] = hm;
   }
-  const int k = blockIdx.x * 64 + cl;
-  const int kc = min(k, K - 1);  // columns past the end read a valid one and are not stored
-  float s = __int_as_float(0x7fc00000);
-  for (int c0 = cg; c0 < chunks; c0 += 16) {
-    float v[4];
+  float s = v[0];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = min(c0 + 4 * j, chunks - 1);  // past the end: repeats the last chunk
-      v[j] = partial[(int64_t)c * K + kc];
-    }
+  for (int j = 1; j < BATCH; ++j) s = fmaxf(s, v[j]);
+  for (int c0 = cg + 4 * BATCH; c0 < chunks; c0 += 4 * BATCH) {  // more than 64 chunks: further rounds
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s = fmaxf(s, v[j]);
+    for (int j = 0; j < BATCH; ++j) v[j] = partial[(int64_t)min(c0 + 4 * j, chunks - 1) * K + kc];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) s = fmaxf(s, v[j]);
   }
   s_part[cg][cl] = s;
   __syncthreads();
