@@ -386,26 +386,37 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn) {
     const bool first_of_group = (t == t_begin) || (gpos == 0);
     const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
+    const int sb = t * 32 + 8 * q;
+
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  The scaled path
+    // loads it here from L2, before the next tile's plane words: memory
+    // operations complete in order, so waiting for A then leaves those in
+    // flight (loaded after them, every tile waited for the prefetch's whole
+    // round trip).
+    u32x4_t A[MT];
+    auto load_a = [&]() {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (A_LATE) {  // rows m >= M read 0
+          const int m = 16 * mt + c;
+          const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + sb) * 2) : 0x80000000u;
+          A[mt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
+        } else if constexpr (AG) {
+          A[mt] = Tc.A[mt];
+        } else {
+          A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
+        }
+      }
+    };
+    if constexpr (A_LATE) {
+      load_a();
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (prefetch) issue(t + PF, Tn);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!A_LATE) load_a();
 
-    const int sb = t * 32 + 8 * q;
     const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[sb]);
-
-    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile]
-    u32x4_t A[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if constexpr (A_LATE) {  // rows m >= M read 0
-        const int m = 16 * mt + c;
-        const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + sb) * 2) : 0x80000000u;
-        A[mt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
-      } else if constexpr (AG) {
-        A[mt] = Tc.A[mt];
-      } else {
-        A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
-      }
-    }
 
     // Rebuild the code bytes (offset binary) and turn them into B operands.
     uint32_t xm[8];
