@@ -92,9 +92,11 @@ int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, in
  * completion counters, fp32 split-K partial sums and, for union batches of
  * more than 16 rows, the per-row grading statistic.  From 512 rows (N a
  * multiple of 64; from 224 rows, as bf16 batches take the library GEMM from
- * there; from 257 rows for N large enough that the fused kernel would need
- * two rounds of blocks) it also holds the dequantized weight (2*N*K bytes)
- * that the library GEMM multiplies.  It must be zero-filled once before its
+ * there; from 257 rows when K <= 8192 or N is large enough that the fused
+ * kernel would need two rounds of blocks) it also holds the dequantized
+ * weight (2*N*K bytes) that the library GEMM multiplies, after the fused
+ * kernel's regions (a shape the library has no algorithm for runs the fused
+ * kernel from the same workspace).  It must be zero-filled once before its
  * first use (every call leaves its counters zero again; the rest needs no
  * initial contents), 256-byte aligned, and calls that share it must be
  * ordered (same stream). */
