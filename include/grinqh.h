@@ -95,8 +95,8 @@ int grinqh_grade(const void* x, int64_t M, int64_t K, int64_t ldx, int dtype, in
  * there; from 257 rows when K <= 8192 or N is large enough that the fused
  * kernel would need two rounds of blocks) it also holds the dequantized
  * weight (2*N*K bytes) that the library GEMM multiplies, after the fused
- * kernel's regions (a shape the library has no algorithm for runs the fused
- * kernel from the same workspace).  It must be zero-filled once before its
+ * kernel's regions (a shape the library has no algorithm for runs the
+ * hand-written prefill kernels from the same workspace).  It must be zero-filled once before its
  * first use (every call leaves its counters zero again; the rest needs no
  * initial contents), 256-byte aligned, and calls that share it must be
  * ordered (same stream). */

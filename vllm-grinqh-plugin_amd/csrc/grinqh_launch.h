@@ -189,7 +189,7 @@ using GemmPrelude = std::function<int(hipStream_t)>;
 // Whether the library offers an algorithm without workspace for this GEMM
 // (asked once per shape and thread, nothing launched).  It offered none for
 // a very deep, narrow product (K = 1048832, N = 64, 512 rows); such products
-// take the fused prefill kernel.
+// take the hand-written prefill kernels (wide-tile or fused).
 bool gemm_x_wt_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int dtype, bool bias, bool alpha_vector);
 int gemm_x_wt(const uint16_t* x, int64_t ldx, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t M,
               int64_t N, int64_t K, int dtype, const float* alpha, hipStream_t st,
