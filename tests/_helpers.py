@@ -94,8 +94,8 @@ def error_stats(y, ref_final: np.ndarray) -> dict:
 
 def record_errors(config: str, case: str, **fields) -> None:
     """Append one error record (JSON line) to the file named by the
-    GRINQH_PARITY_LOG environment variable, if set; tests/parity_report.py
-    turns these records into the per-config error table."""
+    GRINQH_PARITY_LOG environment variable, if set (one JSON object per line:
+    config, case and the error fields)."""
     path = os.environ.get("GRINQH_PARITY_LOG")
     if not path:
         return

@@ -22,15 +22,19 @@ the statistic and grades computed from the whole batch.  Each kernel is held
 to the product it computes with the base tolerance: S10 (scale in fp32) for
 the kernels that apply the scale after the sum, S10 with RNE(w_eff*s) for the
 kernels that round the scaled weight first (as S9 does, grinqh/kernel.py:586).
-The error against the reference's own semantics (S10 for union grading, S9
-for the dense dispatch) is recorded per case (GRINQH_PARITY_LOG).
+Every case is also held to the reference's own semantics (S10 for union
+grading, S9 for the dense dispatch): with the base tolerance plus the bound
+the rounding of the scaled weight to the activation dtype can make,
+u * (|x| @ |w_eff * s|) (one unit of roundoff per weight), since exactly one
+of the two products rounds the weight.  Both errors are recorded per case
+(GRINQH_PARITY_LOG).
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import grinqh_oracle as O
-from tests._helpers import assert_output_close, error_stats, record_errors
+from tests._helpers import UNIT_ROUNDOFF, assert_output_close, error_stats, record_errors
 
 pytestmark = pytest.mark.gpu
 
@@ -92,25 +96,29 @@ def held_rows(M):
 
 def oracle_rows(x_rows, sigma, W, s, t, dtype, graded, rounded):
     """Float64 products of the held rows, column chunk by column chunk: the
-    kernel's own product (``own``) and the reference's (``ref``: S10 for
-    graded, S9 for dense)."""
+    kernel's own product (``own``), the reference's (``ref``: S10 for
+    graded, S9 for dense) and the weight-rounding bound between the two,
+    ``u * (|x| @ |w_eff * s|)``."""
     K, N = W.shape
     xr = x_rows.astype(np.float64)
     bits = O.grade(sigma, t, B) if graded else O.grade(sigma, [-1.0] * 4, B)
     own = np.empty((xr.shape[0], N))
     ref = np.empty((xr.shape[0], N))
+    bound = np.empty((xr.shape[0], N))
     for c0 in range(0, N, COL_CHUNK):
         c1 = min(N, c0 + COL_CHUNK)
         Wc, sc = W[:, c0:c1], s[:, c0:c1]
+        weff = O.effective_weight(Wc, bits, B).astype(np.float64) * np.repeat(sc, GS, 0)[:K]
+        bound[:, c0:c1] = UNIT_ROUNDOFF[dtype] * (np.abs(xr) @ np.abs(weff))
         if graded:
-            exact = xr @ (O.effective_weight(Wc, bits, B).astype(np.float64) * np.repeat(sc, GS, 0)[:K])
+            exact = xr @ weff
             ref[:, c0:c1] = exact
             own[:, c0:c1] = xr @ O.graded_weight_rounded(Wc, bits, sc, B, GS, dtype) if rounded else exact
         else:
             r9 = xr @ O.dense_weight(Wc, sc, GS, dtype)
             ref[:, c0:c1] = r9
             own[:, c0:c1] = r9 if rounded else O.dense_exact_f64(xr, Wc, sc, GS)
-    return own, ref
+    return own, ref, bound
 
 
 def run_case(config, name, K, N, M, x, t, mode, wts):
@@ -123,12 +131,14 @@ def run_case(config, name, K, N, M, x, t, mode, wts):
     sigma = x.abs().float().amax(0).cpu().numpy()  # exact; these inputs hold no NaN
     graded = mode == "union"
     rounded = rounds_weight(M)
-    own, ref = oracle_rows(xn, sigma, W, s, t, "float16", graded, rounded)
+    own, ref, bound = oracle_rows(xn, sigma, W, s, t, "float16", graded, rounded)
     yr = y[torch.from_numpy(rows).cuda()]
     fin_own = O.bias_add(own, None, "float16")
     fin_ref = O.bias_add(ref, None, "float16")
     case = f"{name} K={K} N={N} M={M} {mode}"
     assert_output_close(yr, own, fin_own, "float16", what=case)
+    # the reference's product (S10 / S9), with the weight-rounding bound
+    assert_output_close(yr, ref, fin_ref, "float16", extra_tol=bound, what=case + " against the reference")
     e_own = error_stats(yr, fin_own)
     e_ref = error_stats(yr, fin_ref)
     record_errors(config, case, rows_checked=int(len(rows)), weight_rounded=bool(rounded),

@@ -124,3 +124,29 @@ def test_activations_beyond_32_bit_offsets_rejected(lib):
     assert call(1 << 18, 4096, 4096, 48) == _lib.GRINQH_ERR_INVALID
     # one decode launch: 2 rows of 2^30 halves each
     assert call(2, 32, 1 << 30, 48) == _lib.GRINQH_ERR_INVALID
+
+
+def test_noalloc_rejects_mode_and_thresholds_before_device_state(lib):
+    """The allocation-free entry point validates the mode and, for graded
+    products, the thresholds pointer before it looks up or clears its device
+    scratch: without a GPU such a call returns GRINQH_ERR_INVALID, not the
+    GRINQH_ERR_HIP a device lookup would give."""
+    from grinqh import _lib
+    t = _lib.thresholds_f32([0.0] * 4)
+    dummy = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    # an untyped handle of the same library, so that a null thresholds pointer can be passed
+    fn = ctypes.CDLL(_lib.library_path()).grinqh_gemm_or_gemv_noalloc
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                   ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+
+    def call(mode, thr, M=1):
+        tp = ctypes.cast(thr, ctypes.c_void_p) if thr is not None else None
+        return fn(dummy, M, 4096, 4096, 4096, 0, dummy, dummy, None, dummy, 8, 128, tp, mode, None)
+
+    assert call(9, t) == _lib.GRINQH_ERR_INVALID
+    assert call(-1, t) == _lib.GRINQH_ERR_INVALID
+    assert call(_lib.MODE_UNION, None) == _lib.GRINQH_ERR_INVALID            # graded: thresholds required
+    assert call(_lib.MODE_REFERENCE, None, M=1) == _lib.GRINQH_ERR_INVALID   # one row is graded
+    assert call(_lib.MODE_UNION, t, M=0) == _lib.GRINQH_OK                   # empty batch: nothing to do

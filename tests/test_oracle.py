@@ -376,3 +376,81 @@ def test_cpu_reference_matches_oracle(b):
     yd = C.dense_prefill(torch.from_numpy(x), P, torch.from_numpy(s), 128, b).double().numpy()
     refd = O.dense_prefill(x, W, s, None, 128, "float16")
     np.testing.assert_allclose(yd, refd, rtol=2e-3, atol=2e-3 * np.sqrt(np.mean(refd ** 2)))
+
+
+# --------------------------------------------------------------------------- epilogue
+
+_TDT = {"float16": torch.float16, "bfloat16": torch.bfloat16}
+# an exact sum and a bias whose cast-then-add result (two roundings) differs
+# from one rounding of their sum: fp16 has 11 significant bits, so 2049 lies
+# halfway between 2048 and 2050 and rounds to 2048, and 2048 + 1 rounds to
+# 2048 again, where 2049 + 1 = 2050 is exact; bf16 (8 bits) likewise at 257
+_TWICE_CASES = {"float16": [(2049.0, 1.0, 2048.0, 2050.0), (-2051.0, -1.0, -2052.0, -2052.0),
+                            (4097.0, 3.0, 4100.0, 4100.0), (2051.0, 1.0, 2052.0, 2052.0),
+                            (1025.5, 0.5, 1026.0, 1026.0), (2049.0, 2.0, 2050.0, 2052.0)],
+                "bfloat16": [(257.0, 1.0, 256.0, 258.0), (-513.0, -2.0, -512.0, -516.0),
+                             (259.0, 1.0, 260.0, 260.0), (257.0, 3.0, 260.0, 260.0)]}
+
+
+def _torch_cast_then_add(y32: np.ndarray, bias: np.ndarray, dtype: str) -> np.ndarray:
+    """The reference epilogue in torch on the CPU: the fp32 result cast to the
+    activation dtype, then ``add_`` of the bias in that dtype
+    (grinqh/kernel.py:706-708)."""
+    y = torch.from_numpy(np.asarray(y32, dtype=np.float32)).to(_TDT[dtype])
+    if bias is not None:
+        y.add_(torch.from_numpy(np.asarray(bias, dtype=np.float32)).to(_TDT[dtype]))
+    return y.double().numpy()
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_bias_add_is_cast_then_add(dtype):
+    """O.bias_add against torch's cast-then-add on random fp32 results over
+    many magnitudes (and zeros, infinities), plus targeted values where the two
+    roundings differ from one: the oracle must give the two-rounding value."""
+    rng = np.random.default_rng(21)
+    n = 20000
+    y = (rng.standard_normal(n) * 10.0 ** rng.integers(-4, 5, n)).astype(np.float32)
+    y[:4] = [0.0, -0.0, np.inf, -np.inf]
+    bias = torch.from_numpy((rng.standard_normal(n) * 10.0 ** rng.integers(-4, 5, n)).astype(np.float32))
+    bias = bias.to(_TDT[dtype]).float().numpy()
+    got = O.bias_add(y.astype(np.float64)[None, :], bias, dtype)[0]
+    ref = _torch_cast_then_add(y, bias, dtype)
+    assert np.array_equal(got, ref, equal_nan=True)
+    assert np.array_equal(O.bias_add(y.astype(np.float64)[None, :], None, dtype)[0],
+                          _torch_cast_then_add(y, None, dtype))
+    for v, b, twice, once in _TWICE_CASES[dtype]:
+        yy, bb = np.array([[v]]), np.array([b])
+        assert O.bias_add(yy, bb, dtype)[0, 0] == twice == _torch_cast_then_add(np.float32([v]), bb, dtype)[0]
+        assert O.rne_cast(np.array([v + b]), dtype)[0] == once
+    # the targeted cases are discriminating: at least one of them differs
+    assert any(tw != on for _, _, tw, on in _TWICE_CASES[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_gemv_and_dense_prefill_bias_against_torch(dtype):
+    """The oracle's products with a bias, compared with torch on the CPU on
+    integer operands whose fp32 sums are exact (so no summation order enters):
+    O.gemv against the fp32 GEMV result cast then bias-added
+    (grinqh/kernel.py:697-708), O.dense_prefill against torch's
+    ``x @ Wd`` in the activation dtype followed by ``y.add_(bias)``
+    (:561-587, :707-708).  The operands put many results where the two
+    roundings differ from one, which the test also counts."""
+    rng = np.random.default_rng(22)
+    K, N, b = 256, 256, 8
+    W = _rand_w(rng, K, N, b)
+    s = np.full((K // 128, N), 1.0, dtype=np.float64)
+    x = rng.integers(-3, 4, size=(6, K)).astype(np.float64)
+    bias = rng.integers(-5, 6, size=N).astype(np.float64)
+    tdt = _TDT[dtype]
+    # GEMV (one row, thresholds -1: every zone active, w_eff = W)
+    exact = x[:1] @ W.astype(np.float64)
+    got = O.gemv(x[:1], W, s, bias, [-1.0] * 4, b, 128, dtype)
+    assert np.array_equal(got, _torch_cast_then_add(exact.astype(np.float32), bias, dtype))
+    # dense prefill: torch CPU matmul in the activation dtype, then add_ in that dtype
+    Wd = torch.from_numpy(W.astype(np.float32)).to(tdt)
+    y_t = torch.from_numpy(x.astype(np.float32)).to(tdt) @ Wd
+    y_t.add_(torch.from_numpy(bias.astype(np.float32)).to(tdt))
+    got = O.dense_prefill(x, W, s, bias, 128, dtype)
+    assert np.array_equal(got, y_t.double().numpy())
+    once = O.rne_cast(x @ W.astype(np.float64) + bias[None, :], dtype)
+    assert int((once != got).sum()) > 20

@@ -8,7 +8,6 @@ from tests/vllm_shim, as in tests/test_plugin_surface.py.
 """
 import importlib
 import os
-import sys
 
 import numpy as np
 import pytest
@@ -17,11 +16,7 @@ import torch
 from oracle import grinqh_oracle as O
 from tests._helpers import assert_output_close, dense_rounding_bound, error_stats, record_errors
 
-HERE = os.path.dirname(os.path.abspath(__file__))
-try:
-    import vllm  # noqa: F401
-except ImportError:
-    sys.path.insert(0, os.path.join(HERE, "vllm_shim"))
+import vllm  # noqa: F401  (the real vLLM, or the stand-in tests/conftest.py put on the path)
 
 pytestmark = pytest.mark.gpu
 

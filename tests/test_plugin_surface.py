@@ -9,18 +9,14 @@ anything: there is no CPU fallback in the product.
 import importlib
 import json
 import os
-import sys
 
 import pytest
 import torch
 
+import vllm  # the real vLLM, or the stand-in tests/conftest.py put on the path
+
 HERE = os.path.dirname(os.path.abspath(__file__))
-try:
-    import vllm  # noqa: F401
-    REAL_VLLM = True
-except ImportError:
-    REAL_VLLM = False
-    sys.path.insert(0, os.path.join(HERE, "vllm_shim"))
+REAL_VLLM = not os.path.abspath(vllm.__file__).startswith(os.path.join(HERE, "vllm_shim") + os.sep)
 
 
 @pytest.fixture(scope="module")

@@ -7,9 +7,10 @@
 // op(A) * B with A = Wt (K x N, ld K, transposed) and B = X (K x M, ld ldx),
 // the "TN" form, which ran 10-55 % faster here than the K x N weight.
 //
-// The bias goes through the GEMM's bias epilogue: y = RNE(acc + bias), one
-// rounding, where the reference rounds twice (RNE(RNE(acc) + bias)); the two
-// differ by at most one unit in the last place of y.
+// The product calls it without bias and adds the bias in a pass of its own
+// (launch_add_bias_rows), so that y = RNE(RNE(acc) + bias) rounds twice as
+// the reference's matmul followed by y.add_(bias) does; the GEMM's bias
+// epilogue would round acc + bias once.
 //
 // One hipBLASLt handle per device (created on first use, kept for the
 // process); the descriptors and the chosen algorithm of each shape are
@@ -18,7 +19,10 @@
 // of two) times the heuristic's candidates in the product's own sequence
 // (fastest_candidate) and keeps the fastest: gate_up at 2048 rows 465 -> 428
 // us for the whole product, gate_up and down at 8192 rows ~20 % faster, the
-// other Llama-3-8B shapes unchanged.
+// other Llama-3-8B shapes unchanged.  The summation order of the GEMM
+// depends on the algorithm, so a timed choice trades bit-for-bit
+// reproducibility across processes for speed; GRINQH_GEMM_TUNE=0 (read once)
+// keeps the heuristic's first candidate instead and times nothing.
 //
 // Only algorithms that use no workspace are taken.  The stream-K algorithms
 // the heuristic prefers for the large shapes use one, and a graded gate_up
@@ -28,6 +32,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -267,9 +272,13 @@ bool make_plan(const GemmShape& s, GemmPlan& pl, const GemmCall& call) {
       if (std::memcmp(algos[i].data, e.second.data, sizeof(e.second.data)) == 0) pl.algo = algos[i];
     return true;
   }
+  static const bool tune = [] {
+    const char* v = std::getenv("GRINQH_GEMM_TUNE");
+    return v == nullptr || std::strcmp(v, "0") != 0;
+  }();
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(call.stream, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-  if (cap != hipStreamCaptureStatusNone) {  // nothing is timed during a capture (nor remembered)
+  if (!tune || cap != hipStreamCaptureStatusNone) {  // nothing is timed during a capture (nor remembered)
     pl.algo = algos[0];
     return true;
   }

@@ -138,8 +138,8 @@ bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
   if (wl.library_gemm && use_library_gemm(M, d.K, d.N, dtype) &&
-      gemm_x_wt_supported(M, d.N, d.K, d.ldx, dtype, d.bias != nullptr,
-                          graded && dtype == GRINQH_DTYPE_F16)) {  // the (graded) weight once, then the library GEMM
+      gemm_x_wt_supported(M, d.N, d.K, d.ldx, dtype, /*bias=*/false, graded && dtype == GRINQH_DTYPE_F16) &&
+      (d.bias == nullptr || aligned(d.bias, 16))) {  // the (graded) weight once, then the library GEMM
     // an error a library left in this thread's last-error slot must not be
     // taken for a failure of the launches below
     (void)hipGetLastError();
@@ -164,8 +164,13 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     rc = dequant(st);
     t_kernel_timing = KernelTiming{};
     const GemmPrelude prelude = dequant;
-    if (rc == GRINQH_OK)
-      rc = gemm_x_wt(xs, d.ldx, wt, d.bias, ys, M, d.N, d.K, dtype, alpha, st, &prelude);
+    // the GEMM rounds its output once; the bias follows as its own rounding
+    // (cast, then add, as the reference's y.add_(bias) after the matmul)
+    if (rc == GRINQH_OK) rc = gemm_x_wt(xs, d.ldx, wt, nullptr, ys, M, d.N, d.K, dtype, alpha, st, &prelude);
+    if (rc == GRINQH_OK && d.bias != nullptr) {
+      (void)hipGetLastError();  // a library call may leave an error in this thread's slot
+      rc = launch_add_bias_rows(ys, d.bias, M, d.N, dtype, st);
+    }
     if (rc == GRINQH_OK && graded) {
       (void)hipGetLastError();  // the GEMM's library calls may leave one behind as well
       rc = launch_nonfinite_rows_to_nan(flags, (int)M, d.K, ys, d.N, dtype, st);
@@ -431,9 +436,14 @@ int grinqh_prefill_dense(const void* x, int64_t M, int64_t K, int64_t ldx, int64
 int grinqh_gemm_or_gemv_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype,
                                 const void* planes_u32, const void* scale, const void* bias, void* y, int max_bits,
                                 int group_size, const float thresholds[4], int mode, void* stream) {
-  // arguments first: an invalid call touches no device state
+  // arguments first (shapes, mode, thresholds): an invalid call touches no device state
   int rc = check_product_args(x, M, K, ldx, N, dtype, planes_u32, scale, y, max_bits, group_size);
-  if (rc != GRINQH_OK || M == 0) return rc;
+  if (rc != GRINQH_OK) return rc;
+  if (mode != GRINQH_MODE_REFERENCE && mode != GRINQH_MODE_UNION && mode != GRINQH_MODE_DENSE)
+    return GRINQH_ERR_INVALID;
+  if (M == 0) return GRINQH_OK;
+  const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
+  if (graded && thresholds == nullptr) return GRINQH_ERR_INVALID;
   void* ws = nullptr;
   rc = scratch_on_current_device(&ws, as_stream(stream));
   if (rc != GRINQH_OK) return rc;

@@ -307,6 +307,29 @@ __global__ __launch_bounds__(256) void nonfinite_rows_to_nan_kernel(const uint8_
   for (int n = threadIdx.x; n < N; n += 256) y[(int64_t)m * N + n] = nan;
 }
 
+// y[m][n] = RNE(y[m][n] + bias[n]) in the activation dtype: the bias add of
+// the reference (y.add_(bias) on the matmul's rounded output,
+// grinqh/kernel.py:706-708) after a GEMM that wrote y without bias.  One
+// thread per 8 columns (N % 8 == 0, 16-byte aligned rows).
+template <typename DT>
+__global__ __launch_bounds__(256) void add_bias_rows_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ bias,
+                                                            int64_t M, int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8-column chunk
+  const int cpr = N / 8;
+  if (i >= M * cpr) return;
+  const int64_t m = i / cpr;
+  const int n0 = (int)(i - m * cpr) * 8;
+  u32x4_t v = *reinterpret_cast<const u32x4_t*>(&y[m * N + n0]);
+  const u32x4_t b = *reinterpret_cast<const u32x4_t*>(&bias[n0]);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const float a0 = to_f32<DT>((uint16_t)(v[h] & 0xFFFFu)) + to_f32<DT>((uint16_t)(b[h] & 0xFFFFu));
+    const float a1 = to_f32<DT>((uint16_t)(v[h] >> 16)) + to_f32<DT>((uint16_t)(b[h] >> 16));
+    v[h] = (uint32_t)from_f32<DT>(a0) | ((uint32_t)from_f32<DT>(a1) << 16);
+  }
+  *reinterpret_cast<u32x4_t*>(&y[m * N + n0]) = v;
+}
+
 template <typename DT, bool DENSE>
 int launch_dequant_dt(const DequantParams& p, int max_bits, hipStream_t st) {
   const dim3 grid((unsigned)((p.NW + kDqColsPerBlock - 1) / kDqColsPerBlock),
@@ -353,6 +376,19 @@ int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y
   const uint16_t nan = dtype == GRINQH_DTYPE_BF16 ? 0x7FC0u : 0x7E00u;
   hipLaunchKernelGGL(nonfinite_rows_to_nan_kernel, dim3((unsigned)M), dim3(256), 0, st, flags, (K + 255) / 256, M, y,
                      N, nan);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
+}
+
+int launch_add_bias_rows(uint16_t* y, const uint16_t* bias, int64_t M, int N, int dtype, hipStream_t st) {
+  if (M <= 0 || bias == nullptr) return GRINQH_OK;
+  if (N % 8 != 0 || (reinterpret_cast<uintptr_t>(y) & 15u) || (reinterpret_cast<uintptr_t>(bias) & 15u))
+    return GRINQH_ERR_INVALID;
+  const int64_t chunks = M * (N / 8);
+  const dim3 grid((unsigned)((chunks + 255) / 256));
+  if (dtype == GRINQH_DTYPE_BF16)
+    hipLaunchKernelGGL(add_bias_rows_kernel<BF16>, grid, dim3(256), 0, st, y, bias, M, N);
+  else
+    hipLaunchKernelGGL(add_bias_rows_kernel<F16>, grid, dim3(256), 0, st, y, bias, M, N);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

@@ -177,6 +177,10 @@ inline int sigma_chunk_rows(int64_t M) {
 // n_scale values of scale
 int launch_sigma_chunks(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* partial, uint8_t* flags,
                         float* sigma, const uint16_t* scale, int64_t n_scale, uint32_t* slots, hipStream_t st);
+// y = RNE(y + bias) per row, in the activation dtype (N % 8 == 0, 16-byte
+// aligned y and bias): the library GEMM writes its rounded output without
+// bias, so that the bias add is a second rounding as in the reference
+int launch_add_bias_rows(uint16_t* y, const uint16_t* bias, int64_t M, int N, int dtype, hipStream_t st);
 // after the GEMM: the outputs of every flagged row become NaN
 int launch_nonfinite_rows_to_nan(const uint8_t* flags, int M, int K, uint16_t* y, int N, int dtype, hipStream_t st);
 // y[m][n] = alpha[n] * (x[M][K] @ wt[N][K]^T)[m][n] (+ bias[n]) in the

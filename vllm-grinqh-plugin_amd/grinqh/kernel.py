@@ -50,6 +50,10 @@ def set_batch_grading_mode(mode: str) -> None:
     _BATCH_GRADING = mode
 
 
+def _stream_capturing(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
+
 class _Workspaces:
     """Per (device, stream) workspace: split-K counters and partial sums.
 
@@ -57,35 +61,45 @@ class _Workspaces:
     counters zero between calls).  Calls on one stream are ordered, so they
     may share it; different streams get different buffers.
 
-    A buffer that is outgrown is retired, never freed: a HIP graph captured
-    while it was current keeps its address and writes into it on every
-    replay, so returning it to the allocator would let those replays
-    overwrite whatever tensor is placed there next.  A retired buffer's
-    counters are still zero (every call leaves them so), so such a replay
-    stays correct."""
+    Sizes grow in powers of two (at least 1 MiB), so a caller whose batches
+    keep growing reallocates O(log size) times.  An outgrown buffer is
+    dropped (returned to the allocator) unless a HIP graph was captured while
+    it was current: such a graph keeps its address and writes into it on
+    every replay, so freeing it would let those replays overwrite whatever
+    tensor is placed there next.  Those buffers alone are retired and kept
+    alive; their counters are still zero (every call leaves them so), so such
+    a replay stays correct.  With power-of-two growth the retired bytes of
+    one (device, stream) stay below the size of its current buffer."""
 
-    def __init__(self):
-        self._bufs = {}
+    def __init__(self, capturing=_stream_capturing):
+        self._bufs = {}        # key -> [buffer, captured while current]
         self._retired = []
         self._lock = threading.Lock()
+        self._capturing = capturing
+
+    @staticmethod
+    def _size_for(nbytes: int) -> int:
+        return max(1 << 20, 1 << (int(nbytes) - 1).bit_length())
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
         if nbytes == 0:
             return None
-        key = (device.index, stream)
+        key = (device.type, device.index, stream)
+        capturing = self._capturing(device)
         with self._lock:
-            buf = self._bufs.get(key)
-            if buf is None or buf.numel() < nbytes:
-                if torch.cuda.is_current_stream_capturing():
+            entry = self._bufs.get(key)
+            if entry is None or entry[0].numel() < nbytes:
+                if capturing:
                     raise RuntimeError(
                         "GRINQH: workspace must be allocated before graph capture; run the largest "
                         "batch once eagerly first")
-                size = max(nbytes, 1 << 20)
-                if buf is not None:
-                    self._retired.append(buf)
-                buf = torch.zeros(size, dtype=torch.uint8, device=device)
-                self._bufs[key] = buf
-            return buf
+                if entry is not None and entry[1]:
+                    self._retired.append(entry[0])
+                entry = [torch.zeros(self._size_for(nbytes), dtype=torch.uint8, device=device), False]
+                self._bufs[key] = entry
+            if capturing:
+                entry[1] = True
+            return entry[0]
 
     def retired_bytes(self) -> int:
         """Bytes held by outgrown workspaces (kept alive for captured graphs)."""
