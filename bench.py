@@ -86,6 +86,15 @@ def thresholds_for(x, q=(0.5, 0.8, 0.95)):
     return [0.0] + [float(v) for v in np.quantile(sigma, q)]
 
 
+def prefill_kernel_name(M, K, N, mode, noalloc=False):
+    """The kernel the dispatch picks for an fp16 product of this shape."""
+    from grinqh import _lib
+    kern, rows, splits = _lib.product_kernel(M, K, K, N, _lib.DTYPE_F16, BITS, GS,
+                                             _lib.MODE_UNION if mode == "union" else _lib.MODE_DENSE, noalloc)
+    name = _lib.KERNEL_NAMES[kern]
+    return f"{name} ({rows}-row blocks, {splits} K ranges)" if kern == _lib.KERNEL_TALL else name
+
+
 def library_free_product(torch, lib, x, P, s, t, mode):
     """One product through grinqh_gemm_or_gemv_noalloc (include/grinqh.h): no
     workspace, so no dense weight for the library GEMM; fp16 batches of 512
@@ -413,17 +422,35 @@ def main() -> int:
             call = lambda: library_free_product(torch, lib, x, P, s, t, mode)
         else:
             call = lambda: run_product(x, P, s, None, BITS, GS, N // 4, t, mode)
-        for _ in range(2):
+        for _ in range(3):
             call()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(2):
+        for _ in range(10):
             call()
         e1.record()
         e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / 2
-        log(f"prefill case {args.prefill_case}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s")
+        us = e0.elapsed_time(e1) * 1e3 / 10
+        # the main kernel alone: events the dispatch records around its launch
+        lib = _lib.load_library()
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+        for a, b in pairs:
+            a.record()
+            b.record()
+        torch.cuda.synchronize()
+        for a, b in pairs:
+            _lib.check(lib.grinqh_time_next_product(ctypes.c_void_p(a.cuda_event), ctypes.c_void_p(b.cuda_event)),
+                       "grinqh_time_next_product")
+            call()
+        torch.cuda.synchronize()
+        k_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in pairs]))
+        kern, wm, splits = _lib.product_kernel(M, K, K, N, _lib.DTYPE_F16, BITS, GS,
+                                               _lib.MODE_UNION if mode == "union" else _lib.MODE_DENSE,
+                                               noalloc=path == ["noalloc"])
+        log(f"prefill case {args.prefill_case}: {us:.1f} us {2 * M * K * N / us / 1e6:.1f} TFLOP/s; "
+            f"main kernel {_lib.KERNEL_NAMES[kern]} (wm {wm}, splits {splits}) {k_us:.1f} us "
+            f"{2 * M * K * N / k_us / 1e6:.1f} TFLOP/s")
         return 0
 
     # ---------------- weights: a pool of >= POOL_BYTES of copies per shape, handed out LRU
@@ -601,9 +628,10 @@ def main() -> int:
             x = synth_x(torch, PREFILL_M, K, 99 + i, dev)
             us = prefill_time_us(name, K, N, PREFILL_M, x, [0.0] * 4, "dense", 5)
             tf = 2.0 * PREFILL_M * K * N / (us * 1e-6) / 1e12
+            kern = prefill_kernel_name(M=PREFILL_M, K=K, N=N, mode="dense")
             prefill.append({"shape": name, "M": PREFILL_M, "us": round(us, 2), "tflops": round(tf, 1),
-                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
-            log(f"prefill {name:8s} M={PREFILL_M} {us:9.1f} us {tf:7.1f} TFLOP/s")
+                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "kernel": kern})
+            log(f"prefill {name:8s} M={PREFILL_M} {us:9.1f} us {tf:7.1f} TFLOP/s ({kern})")
 
     # ---------------- graded prefill sweep: union grading with the
     # 70/20/8/2% grade mix (t = [0, P70, P90, P98] of the batch statistic)
@@ -616,23 +644,25 @@ def main() -> int:
                 t = thresholds_for(x, (0.7, 0.9, 0.98))
                 us = prefill_time_us(name, K, N, M, x, t, "union", 3)
                 tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
+                kern = prefill_kernel_name(M=M, K=K, N=N, mode="union")
                 prefill_graded.append({"shape": name, "M": M, "us": round(us, 2), "tflops": round(tf, 1),
-                                       "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
-                log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s")
+                                       "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "kernel": kern})
+                log(f"prefill graded {name:8s} M={M:5d} {us:9.1f} us {tf:7.1f} TFLOP/s ({kern})")
                 del x
     # MFMA leg of the metric (M=2048): the largest product, gate_up, priced on
-    # its whole graph-timed time (dequantization pass + library GEMM; the
-    # kernels' own times are in profiles/prefill_gate_up_m2048_kernel_stats.md)
+    # its whole graph-timed time (the default dispatch at 2048 rows: the
+    # dequantization pass + library GEMM)
     roofline_prefill = None
     if prefill:
         g = max(prefill, key=lambda r: r["us"])
         roofline_prefill = {"bound": "mfma", "achieved": g["tflops"], "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                            "frac": g["frac"], "traffic": None, "shape": g["shape"], "M": g["M"],
-                            "measured": "graph-timed product: dequantization pass + library GEMM, rotated weights"}
+                            "frac": g["frac"], "traffic": None, "shape": g["shape"], "M": g["M"], "kernel": g["kernel"],
+                            "measured": "graph-timed product, rotated weights"}
 
     # ---------------- the same products without the library path (allocation-free
-    # entry point: no dense weight; the wide-tile kernel where its grid fills the
-    # GPU), eager, rotated copies
+    # entry point: no dense weight; the hand-written large-batch kernel
+    # prefill_tall_kernel wherever its repacked x fits the fixed scratch),
+    # eager, rotated copies
     prefill_library_free = None
     if not args.no_prefill and not args.no_library_free:
         prefill_library_free = []
@@ -656,12 +686,21 @@ def main() -> int:
                 e1.synchronize()
                 us = e0.elapsed_time(e1) * 1e3 / n_it
                 tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
-                kernel = "prefill_wide_kernel" if (N // 256) * -(-M // 256) >= 192 else "prefill_kernel"
+                kernel = prefill_kernel_name(M=M, K=K, N=N, mode=mode, noalloc=True)
                 prefill_library_free.append({"shape": name, "M": M, "mode": mode, "us": round(us, 2),
                                              "tflops": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                                              "kernel": kernel})
                 log(f"prefill library-free {name:8s} M={M} {mode:5s} {us:9.1f} us {tf:7.1f} TFLOP/s ({kernel})")
                 del x
+    # the hand-written large-batch kernel on the largest product (without a
+    # workspace: repack pass + kernel, whole tiles)
+    roofline_prefill_tall = None
+    if prefill_library_free:
+        g = max((r for r in prefill_library_free if r["mode"] == "dense"), key=lambda r: r["us"])
+        roofline_prefill_tall = {"bound": "mfma", "achieved": g["tflops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": g["frac"], "traffic": None, "shape": g["shape"],
+                                 "M": g["M"], "kernel": g["kernel"],
+                                 "measured": "eager allocation-free calls (x repack + kernel), rotated weights"}
     prefill_min_gap = rot.min_gap
     del pools, rot
     torch.cuda.empty_cache()
@@ -788,6 +827,7 @@ def main() -> int:
         "prefill": prefill,
         "prefill_graded": prefill_graded,
         "roofline_prefill": roofline_prefill,
+        "roofline_prefill_tall": roofline_prefill_tall,
         "prefill_library_free": prefill_library_free,
         "llama70b_adversarial": big,
         "llama8b_decode_step": model_step,

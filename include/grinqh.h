@@ -190,6 +190,26 @@ int grinqh_gemm_or_gemv_noalloc(const void* x, int64_t M, int64_t K, int64_t ldx
  * NULLs disarms.  Not for use under graph capture. */
 int grinqh_time_next_product(void* event_before, void* event_after);
 
+/* Kernel selection query; no counterpart in the reference (for tests and
+ * benchmarks).  Names the kernel that serves an M-row product of this shape
+ * through grinqh_gemm_or_gemv (noalloc = 0) or grinqh_gemm_or_gemv_noalloc
+ * (noalloc = 1), nothing launched: GRINQH_KERNEL_GEMV (1-4 rows per launch),
+ * GRINQH_KERNEL_DECODE (5-64), GRINQH_KERNEL_TALL (the large-batch prefill;
+ * *rows_per_block and *splits receive its plan), GRINQH_KERNEL_LIBRARY (the
+ * dense weight and the library GEMM, where the dispatch prefers it; the
+ * library's algorithm query at run time can still send the call to the fused
+ * prefill) or GRINQH_KERNEL_FUSED (the fused prefill).  GRINQH_PREFILL=tall or
+ * =library in the environment forces the large-batch kernel or the library
+ * path where they apply, as for the products.  Returns the kernel id, or a
+ * negative status for bad arguments. */
+#define GRINQH_KERNEL_GEMV 1
+#define GRINQH_KERNEL_DECODE 2
+#define GRINQH_KERNEL_TALL 3
+#define GRINQH_KERNEL_LIBRARY 4
+#define GRINQH_KERNEL_FUSED 5
+int grinqh_product_kernel(int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, int max_bits, int group_size,
+                          int mode, int noalloc, int* rows_per_block, int* splits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,25 +57,86 @@ def test_workspace_query(lib):
     assert lib.grinqh_workspace_bytes(200, 4096, 4096, 8, 1) >= lib.grinqh_workspace_bytes(200, 4096, 4096, 8, 2)
 
 
-def test_workspace_query_library_gemm_path(lib):
-    """The large-batch prefill path (dequantized weight + library GEMM) sizes
-    the workspace for the K-contiguous weight (2*N*K bytes) after the fused
-    kernel's regions (the GEMM itself takes no workspace).  The query has no dtype, so it
-    covers the path whenever either dtype may take it: from 512 rows, from
-    224 in bf16, at 257-511 rows when K <= 8192 or the fused grid would need
-    more than one round (gate_up's N); never when N / 16 is not a multiple of
-    4; dense and union alike."""
-    K = 4096
+def test_workspace_query_library_gemm_path(lib, monkeypatch):
+    """A prefill takes the library path (the dense weight, 2*N*K bytes, in
+    the workspace) where the dispatch prefers it -- from 513 rows, and at
+    512 rows and below for weights under 2^25 elements -- and the library has
+    an algorithm for the shape (from 512 rows, from 224 in bf16); the
+    large-batch kernel where it applies otherwise (K % 64 == 0,
+    N % 128 == 0, from 256 rows: no dense weight, only the split-K counters,
+    the statistic, the partial sums of the tiles split over K and the
+    activations repacked in MFMA fragment order, 2 bytes per element with
+    rows rounded up to 16); the fused kernel, whose partial sums the layout
+    also covers, for the rest.  GRINQH_PREFILL=tall or =library forces
+    either."""
     dense, union = 2, 1
-    library = lambda M, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode) >= 2 * N * K
+    q = lambda M, K, N, mode: lib.grinqh_workspace_bytes(M, K, N, 8, mode)
     for mode in (dense, union):
-        assert library(512, 6144, mode) and library(2048, 28672, mode) and library(300, 28672, mode)
-        assert library(224, 6144, mode) and not library(223, 6144, mode) and not library(128, 28672, mode)
-        assert not library(4096, 4112, mode)
-    # the union layout adds sigma, its chunk maxima and the row flags to the dense one
-    assert lib.grinqh_workspace_bytes(2048, K, 6144, 8, union) > lib.grinqh_workspace_bytes(2048, K, 6144, 8, dense)
-    # the fused kernel's split-K partials stay in front of the library regions
-    assert lib.grinqh_workspace_bytes(240, K, 4096, 8, dense) >= 2 * 4096 * K + 8 * 240 * 4096 * 4
+        head = 16384 + (0 if mode == dense else 4096 * 4)
+        # the library path by default: the dense weight
+        assert q(2048, 4096, 28672, mode) >= 2 * 28672 * 4096
+        assert q(1024, 4096, 6144, mode) >= 2 * 6144 * 4096
+        assert q(512, 4096, 6144, mode) >= 2 * 6144 * 4096   # qkv: under 2^25 elements
+        # gate_up x 512 (2^26.8 elements): the large-batch kernel, 224 tiles
+        # of 512 x 128 in one round, x repacked
+        assert q(512, 4096, 28672, mode) == head + 512 * 4096 * 2
+        # shapes the library has no algorithm for (fewer than 512 rows in fp16
+        # and 224 in bf16) take the large-batch kernel from 256 rows
+        assert q(256, 4096, 6144, mode) < 2 * 6144 * 4096
+        # K % 64 == 32 or N % 128 == 64: the library path's dense weight
+        assert q(512, 4128, 6144, mode) >= 2 * 6144 * 4128
+        assert q(2048, 4096, 4160, mode) >= 2 * 4160 * 4096
+        assert q(224, 4128, 6144, mode) >= 2 * 6144 * 4128 and q(223, 4128, 6144, mode) < 2 * 6144 * 4128
+        assert q(4096, 4128, 4112, mode) < 2 * 4112 * 4128
+    monkeypatch.setenv("GRINQH_PREFILL", "tall")
+    for mode in (dense, union):
+        head = 16384 + (0 if mode == dense else 4096 * 4)
+        # gate_up x 2048: 896 tiles of 512 x 128, the last 128 in two K ranges
+        # (partial sums: 128 tiles x 2 ranges x 256 KiB), then x repacked
+        assert q(2048, 4096, 28672, mode) == head + 128 * 2 * 512 * 128 * 4 + 2048 * 4096 * 2
+        assert q(2040, 4096, 28672, mode) == q(2048, 4096, 28672, mode)
+    # a K split of the large-batch kernel (two 128-column tiles at 512 rows)
+    assert q(512, 4096, 256, dense) >= 2 * 512 * 256 * 4
+    monkeypatch.setenv("GRINQH_PREFILL", "library")
+    assert q(512, 4096, 28672, dense) >= 2 * 28672 * 4096
+    # the union layout adds the statistic to the dense one
+    assert q(2048, 4096, 6144, union) > q(2048, 4096, 6144, dense)
+
+
+def test_product_kernel_query(lib, monkeypatch):
+    """grinqh_product_kernel names the kernel each row count and shape takes,
+    without a GPU: GEMV to 4 rows, decode to 64, the fused prefill below 256
+    rows, the library GEMM or the large-batch kernel above as the dispatch
+    prefers, the large-batch kernel without a workspace (where its repacked
+    activations fit the fixed scratch), the fused kernel where neither
+    fits."""
+    from grinqh import _lib
+    f = lambda M, K, N, mode=_lib.MODE_DENSE, noalloc=False, gs=128: _lib.product_kernel(
+        M, K, K, N, _lib.DTYPE_F16, 8, gs, mode, noalloc)
+    assert f(1, 4096, 4096)[0] == _lib.KERNEL_GEMV
+    assert f(64, 4096, 4096)[0] == _lib.KERNEL_DECODE
+    assert f(200, 4096, 4096)[0] == _lib.KERNEL_FUSED
+    assert f(2048, 4096, 28672)[0] == _lib.KERNEL_LIBRARY
+    assert f(512, 4096, 6144)[0] == _lib.KERNEL_LIBRARY
+    assert f(512, 4096, 28672) == (_lib.KERNEL_TALL, 512, 1)
+    assert f(512, 14336, 4096)[0] == _lib.KERNEL_TALL           # down
+    assert f(256, 4096, 6144)[0] == _lib.KERNEL_TALL            # no library algorithm in fp16
+    # without a workspace: no room for the partial sums of the split tiles
+    assert f(2048, 4096, 28672, _lib.MODE_UNION, noalloc=True) == (_lib.KERNEL_TALL, 512, 1)
+    assert f(4096, 4096, 4112, noalloc=True)[0] == _lib.KERNEL_FUSED
+    # ... and the repacked activations must fit the fixed scratch
+    assert f(8192, 4096, 4096, noalloc=True)[0] == _lib.KERNEL_FUSED
+    assert f(4096, 4096, 4096, noalloc=True)[0] == _lib.KERNEL_TALL
+    monkeypatch.setenv("GRINQH_PREFILL", "tall")
+    # 896 tiles: three full rounds whole, the last 128 tiles in two K ranges
+    assert f(2048, 4096, 28672) == (_lib.KERNEL_TALL, 512, 2)
+    assert f(8192, 4096, 28672) == (_lib.KERNEL_TALL, 512, 1)  # 3584 tiles: 14 full rounds
+    assert f(512, 4096, 256)[0] == _lib.KERNEL_TALL and f(512, 4096, 256)[2] > 1
+    assert f(512, 4096, 2048, gs=32)[0] == _lib.KERNEL_FUSED
+    monkeypatch.setenv("GRINQH_PREFILL", "library")
+    assert f(512, 4096, 28672)[0] == _lib.KERNEL_LIBRARY
+    with pytest.raises(ValueError):
+        f(512, 4016, 4096)  # K % 32 != 0
 
 
 def test_invalid_arguments_rejected_on_host(lib):

@@ -8,8 +8,8 @@ cannot see.  Here the operands are small integers, the codes are 8-bit and the
 scales powers of two, so every product and every partial sum is exact in fp32
 whatever the summation order, and the only roundings left are the epilogue's.
 Each path -- the graded GEMV (1 row), the four-row GEMV, the decode kernels
-(5-64 rows), the fused prefill (65-511), the library-GEMM prefill and the
-hand-written large-batch prefill (512 rows and more, with and without a
+(5-64 rows), the fused prefill (65-255), the library-GEMM prefill and the
+hand-written large-batch prefill (256 rows and more, with and without a
 workspace) -- must then equal the oracle's cast-then-add bit for bit, in
 fp16 and bf16, dense and graded.  The test also counts the outputs where one
 rounding would have given another value, so it cannot pass vacuously.
@@ -96,9 +96,11 @@ CASES = [
     (64, 1024, 2048, "union", "op"),       # decode kernel, four m-tiles
     (100, 512, 1024, "dense", "op"),       # fused prefill
     (200, 512, 1024, "union", "op"),       # graded fused prefill
-    (512, 512, 1024, "dense", "op"),       # large batch, with a workspace
-    (600, 256, 2048, "union", "op"),       # graded large batch, with a workspace
-    (2048, 256, 6144, "dense", "noalloc"),  # large batch without a workspace
+    (512, 512, 1024, "dense", "op"),       # library GEMM prefill (the default for this shape)
+    (600, 256, 2048, "union", "op"),       # graded library GEMM prefill
+    (512, 512, 1024, "dense", "tall"),     # hand-written large-batch kernel, with a workspace
+    (600, 256, 2048, "union", "tall"),
+    (2048, 256, 6144, "dense", "noalloc"),  # large-batch kernel without a workspace
     (2048, 256, 6144, "union", "noalloc"),
 ]
 
@@ -106,8 +108,16 @@ CASES = [
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 @pytest.mark.parametrize("M,K,N,mode,entry", CASES,
                          ids=[f"{c[3]}-M{c[0]}-{c[4]}" for c in CASES])
-def test_epilogue_is_cast_then_add_bit_exact(lib, M, K, N, mode, entry, dtype):
+def test_epilogue_is_cast_then_add_bit_exact(lib, M, K, N, mode, entry, dtype, monkeypatch):
+    from grinqh import _lib
     from grinqh.kernel import run_product
+    dt = _lib.DTYPE_F16 if dtype == "float16" else _lib.DTYPE_BF16
+    mc = {"reference": _lib.MODE_REFERENCE, "union": _lib.MODE_UNION, "dense": _lib.MODE_DENSE}[mode]
+    if entry == "tall":
+        monkeypatch.setenv("GRINQH_PREFILL", "tall")
+    if M >= 512:  # the case reaches the kernel it names
+        want_kernel = _lib.KERNEL_LIBRARY if entry == "op" else _lib.KERNEL_TALL
+        assert _lib.product_kernel(M, K, K, N, dt, B, 128, mc, entry == "noalloc")[0] == want_kernel
     W, x, s, bias = _operands(M * 31 + N + K, M, K, N)
     want, n_differ = _expected(x, W, s, bias, mode, dtype)
     assert n_differ > 0, "operands put no output where one rounding differs from two"

@@ -1,6 +1,10 @@
 // extern "C" entry points of libgrinqh_hip.so (declared in include/grinqh.h):
 // argument validation, workspace carving and kernel selection.
+#include <stdlib.h>
 #include <string.h>
+
+#include <cstdlib>
+#include <cstring>
 
 #include <mutex>
 
@@ -55,8 +59,25 @@ struct WorkspaceLayout {
   // the regions the fused prefill uses
   size_t chunk_off, flag_off, range_off, wt_off;
   bool library_gemm;
+  bool tall;       // the large-batch prefill kernel serves the product (prefill_tall.hip)
+  TallPlan tall_plan;
+  size_t xt_off;   // its repacked activations (after the partial sums)
   DecodePlan plan;
 };
+
+// Which kernel serves a large batch that both can.  Measured on MI355X
+// (random fp16 data, kernel times): the dense weight plus the library GEMM
+// wins from 1024 rows on every Llama-3-8B shape and at 512 rows for the
+// smaller weights (qkv, o_proj); the hand-written large-batch kernel wins at
+// 512 rows for gate_up and down (132 vs 166 us, 104 vs 119 us), where the
+// library path's dequantization pass is a large share.  GRINQH_PREFILL=tall
+// or =library forces one (read on every call, so a test can pin a path).
+bool prefill_prefers_library(int64_t M, int64_t K, int64_t N) {
+  const char* e = std::getenv("GRINQH_PREFILL");
+  if (e != nullptr && std::strcmp(e, "tall") == 0) return false;
+  if (e != nullptr && std::strcmp(e, "library") == 0) return true;
+  return M > 512 || K * N < ((int64_t)1 << 25);
+}
 
 // Plan of one launch of mc rows: the GEMV kernel up to kGemvMaxRows rows, the
 // decode kernel above.  group_size 32 gives the largest GEMV workspace.
@@ -70,31 +91,63 @@ int launch_main(const DecodeParams& p, const DecodePlan& plan, int max_bits, int
 }
 
 // [split-K counters (kCounterBytes, zero between calls) | sigma (K floats,
-// graded batches above kDecodeMaxRows) | split-K partials | library-GEMM
-// regions].  The counters sit at offset 0 for every shape, so a workspace
-// shared by calls of different shapes keeps them zero.  The size does not
-// depend on the dtype: when either dtype may take the library path (bf16
-// from fewer rows) its regions follow those of the fused kernel, so either
-// path runs from the same workspace.
-WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow_library = true) {
+// graded batches above kDecodeMaxRows) | split-K partials | repacked x of
+// the large-batch kernel, or the library-GEMM regions].  The counters sit at
+// offset 0 for every shape, so a workspace shared by calls of different
+// shapes keeps them zero.  The size does not depend on the dtype: when either
+// dtype may take the library path (bf16 from fewer rows) its regions follow
+// those of the fused kernel, so either path runs from the same workspace.
+//
+// A prefill takes the library path where prefill_prefers_library says so and
+// the library has an algorithm for the shape, else the large-batch kernel
+// where it applies, else the fused kernel; without a workspace
+// (allow_library = false) the large-batch kernel whenever it applies.  The
+// large-batch kernel's shape conditions on K and N are known to the workspace
+// query; the group size and ldx are not, so the partial-sum region covers
+// both the large-batch kernel's split (within `budget`, the allocation-free
+// entry point's scratch; 0: a caller-sized workspace) and the fused kernel's,
+// so that any call of the queried (M, K, N, mode) runs in it.
+WorkspaceLayout layout_for(int64_t M, int64_t K, int64_t N, int mode, bool allow_library = true,
+                           int64_t ldx = -1, int gs = -1, size_t budget = 0) {
   WorkspaceLayout w{};
-  size_t partial = 0;
+  size_t partial = 0, xt = 0;
+  const bool g = mode == GRINQH_MODE_UNION;
+  const bool need_sigma = g && M > kDecodeMaxRows;  // the prefill's statistic pass
+  const size_t head = kCounterBytes + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
+  // where the large-batch kernel applies the library path needs an algorithm
+  // for both dtypes (the layout serves either); elsewhere for either
+  const bool lib_f16 = use_library_gemm(M, K, N, GRINQH_DTYPE_F16), lib_bf16 = use_library_gemm(M, K, N, GRINQH_DTYPE_BF16);
+  const bool tall_fits = M > kDecodeMaxRows && prefill_tall_applies(M, K, N, K, 128);
+  const bool lib_first = allow_library && M > kDecodeMaxRows &&
+                         (tall_fits ? lib_f16 && lib_bf16 && prefill_prefers_library(M, K, N) : lib_f16 || lib_bf16);
+  bool tall_shape = false;
   if (M <= kDecodeMaxRows) {
     w.plan = plan_launch(M > 0 ? M : 1, K, N, 32);
     partial = w.plan.splits > 1 ? w.plan.workspace : 0;
   } else {  // prefill: partial sums only when its grid is split over K
-    const int splits = prefill_splits(M, K, N);
-    partial = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+    tall_shape = !lib_first && tall_fits;
+    xt = tall_shape ? round_up(tall_x_bytes(M, K), 256) : 0;
+    if (tall_shape && budget != 0 && head + xt > budget) tall_shape = false, xt = 0;  // no room for x repacked
+    w.tall = tall_shape && ldx >= 0 && gs > 0 && prefill_tall_applies(M, K, N, ldx, gs);
+    if (tall_shape) {
+      const size_t room = budget == 0 ? kMaxPrefillPartialBytes : budget - head - xt;
+      w.tall_plan = plan_tall(M, K, N, room);
+      partial = tall_partial_bytes(w.tall_plan, M, N);
+    }
+    if (!w.tall) {  // the fused kernel (a call that cannot take the large-batch kernel)
+      const int splits = prefill_splits(M, K, N);
+      const size_t fused = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+      partial = fused > partial ? fused : partial;
+    }
   }
-  const bool g = mode == GRINQH_MODE_UNION;
-  const bool need_sigma = g && M > kDecodeMaxRows;  // the prefill's statistic pass
   w.counter_off = 0;
   w.sigma_off = kCounterBytes;
-  w.partial_off = w.sigma_off + (need_sigma ? round_up((size_t)K * sizeof(float), 256) : 0);
-  w.total = (partial == 0 && !need_sigma) ? 0 : w.partial_off + partial;
-  w.library_gemm = allow_library && M > kDecodeMaxRows &&
+  w.partial_off = head;
+  w.xt_off = round_up(w.partial_off + partial, 256);
+  w.total = (partial == 0 && !need_sigma && xt == 0) ? 0 : w.xt_off + xt;
+  w.library_gemm = allow_library && !tall_shape && M > kDecodeMaxRows &&
                    (use_library_gemm(M, K, N, GRINQH_DTYPE_F16) || use_library_gemm(M, K, N, GRINQH_DTYPE_BF16));
-  if (w.library_gemm) {
+  if (w.library_gemm) {  // (no repacked x: the large-batch kernel cannot take these shapes)
     const int64_t chunks = (M + sigma_chunk_rows(M) - 1) / sigma_chunk_rows(M);
     w.chunk_off = round_up(w.partial_off + partial, 256);
     w.flag_off = w.chunk_off + (g ? round_up((size_t)chunks * (size_t)K * sizeof(float), 256) : 0);
@@ -137,6 +190,38 @@ bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64
 // the fused kernel's regions in front of the library path's, so either runs.
 int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t M, int dtype, int max_bits,
                 bool graded, char* ws, const WorkspaceLayout& wl, hipStream_t st) {
+  if (wl.tall) {  // the large-batch kernel: x repacked (graded: the batch statistic first)
+    uint16_t* xt = reinterpret_cast<uint16_t*>(ws + wl.xt_off);
+    int rc = launch_repack_x(xs, d.ldx, (int)M, d.K, xt, st);
+    if (rc != GRINQH_OK) return rc;
+    PrefillParams p{};
+    p.x = xt;
+    p.ldx = d.K;
+    p.planes = d.planes;
+    p.scale = d.scale;
+    p.bias = d.bias;
+    p.y = ys;
+    p.thr = d.thr;
+    p.M = (int)M;
+    p.K = d.K;
+    p.N = d.N;
+    p.NW = d.NW;
+    p.gs = d.gs;
+    p.splits = wl.tall_plan.splits;
+    p.dp_tiles = wl.tall_plan.dp_tiles;
+    p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
+    p.counters = p.splits > 1 ? reinterpret_cast<uint32_t*>(ws + wl.counter_off) : nullptr;
+    if (graded) {
+      float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
+      rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
+      if (rc != GRINQH_OK) return rc;
+      p.sigma = sigma;
+    }
+    arm_kernel_timing();
+    rc = launch_prefill_tall(p, wl.tall_plan, max_bits, dtype, !graded, st);
+    t_kernel_timing = KernelTiming{};
+    return rc;
+  }
   if (wl.library_gemm && use_library_gemm(M, d.K, d.N, dtype) &&
       gemm_x_wt_supported(M, d.N, d.K, d.ldx, dtype, /*bias=*/false, graded && dtype == GRINQH_DTYPE_F16) &&
       (d.bias == nullptr || aligned(d.bias, 16))) {  // the (graded) weight once, then the library GEMM
@@ -235,7 +320,8 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
   if (graded && thresholds == nullptr) return GRINQH_ERR_INVALID;
 
-  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE, allow_library);
+  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE, allow_library,
+                                        ldx, group_size, allow_library ? 0 : ws_bytes);
   if (wl.total > 0 && (workspace == nullptr || ws_bytes < wl.total || !aligned(workspace, 256)))
     return allow_library ? GRINQH_ERR_WORKSPACE : GRINQH_ERR_SCRATCH;
   hipStream_t st = as_stream(stream);
@@ -485,6 +571,32 @@ int grinqh_gemv_batch_union_sigma(const void* x, int64_t M, int64_t K, int64_t l
   if (sigma_chunks == nullptr || !aligned(sigma_chunks, 4)) return GRINQH_ERR_INVALID;
   return run_product(x, M, K, ldx, N, dtype, planes_u32, scale, bias, y, max_bits, group_size, thresholds,
                      GRINQH_MODE_UNION, workspace, workspace_bytes, stream, /*allow_library=*/true, sigma_chunks);
+}
+
+int grinqh_product_kernel(int64_t M, int64_t K, int64_t ldx, int64_t N, int dtype, int max_bits, int group_size,
+                          int mode, int noalloc, int* rows_per_block, int* splits) {
+  const void* nz = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));  // stands for valid pointers
+  if (M < 1 || check_product_args(nz, M, K, ldx, N, dtype, nz, nz, const_cast<void*>(nz), max_bits, group_size) !=
+                   GRINQH_OK)
+    return -GRINQH_ERR_INVALID;
+  if (mode != GRINQH_MODE_REFERENCE && mode != GRINQH_MODE_UNION && mode != GRINQH_MODE_DENSE)
+    return -GRINQH_ERR_INVALID;
+  if (rows_per_block != nullptr) *rows_per_block = 0;
+  if (splits != nullptr) *splits = 0;
+  if (M <= kDecodeMaxRows) return M <= kGemvMaxRows ? GRINQH_KERNEL_GEMV : GRINQH_KERNEL_DECODE;
+  const bool graded = mode == GRINQH_MODE_UNION;
+  const bool allow_library = noalloc == 0;
+  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE, allow_library, ldx,
+                                        group_size, allow_library ? 0 : kScratchBytes);
+  if (wl.tall) {
+    if (rows_per_block != nullptr) *rows_per_block = 64 * wl.tall_plan.rt;
+    if (splits != nullptr) *splits = wl.tall_plan.splits;
+    return GRINQH_KERNEL_TALL;
+  }
+  // (the library's own algorithm query, made at run time on the device, can
+  // still send such a call to the fused kernel)
+  if (wl.library_gemm && use_library_gemm(M, K, N, dtype)) return GRINQH_KERNEL_LIBRARY;
+  return GRINQH_KERNEL_FUSED;
 }
 
 int grinqh_time_next_product(void* event_before, void* event_after) {

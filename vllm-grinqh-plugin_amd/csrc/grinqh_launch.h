@@ -92,6 +92,8 @@ struct PrefillParams {
   int splits;            // grid.z: K ranges (1: y written directly)
   int stages_per_split;  // set by launch_prefill
   float* partial;        // [splits][M][N] fp32 when splits > 1 (the reduce kernel follows)
+  uint32_t* counters;    // tall kernel with splits > 1: per split tile, zero on entry
+  int dp_tiles;          // tall kernel: tiles computed whole, before the split ones
 };
 
 // Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.  p.splits
@@ -106,6 +108,36 @@ int prefill_block_rows(int64_t M, int64_t N);
 // only on (M, K, N), so the workspace size does too.
 constexpr size_t kMaxPrefillPartialBytes = size_t(256) << 20;
 int prefill_splits(int64_t M, int64_t K, int64_t N);
+
+// Large-batch prefill (prefill_tall.hip): (64 * rt) x 128 output tiles over
+// four waves (one per SIMD), x repacked into MFMA fragments and loaded
+// straight into registers, the weight dequantized per 64-row stage into LDS
+// and shared by the block's waves.  From kTallPrefillRows rows, K and the
+// group size multiples of 64, N % 128 == 0 and the repacked x below 2^31
+// bytes.  The first dp_tiles tiles run whole; the others (the last, partly
+// filled round) split K into `splits` ranges, completed in the kernel
+// (partial sums, per-tile counters).
+constexpr int64_t kTallPrefillRows = 256;
+constexpr int kTallDoneBase = kMaxCounters / 2;  // counters: arrivals [0, 2048), done [2048, 4096)
+struct TallPlan {
+  int rt;        // 16-row tiles per wave: 8 (512-row blocks) or 4 (256-row blocks)
+  int splits;    // K ranges of the split tiles
+  int dp_tiles;  // tiles computed whole (all when splits == 1)
+  int tiles;     // output tiles
+};
+bool prefill_tall_applies(int64_t M, int64_t K, int64_t N, int64_t ldx, int gs);
+// max_partial: bytes available for split-K partial sums
+TallPlan plan_tall(int64_t M, int64_t K, int64_t N, size_t max_partial);
+inline size_t tall_partial_bytes(const TallPlan& pl, int64_t M, int64_t N) {
+  (void)M, (void)N;
+  return pl.splits > 1 ? (size_t)(pl.tiles - pl.dp_tiles) * (size_t)pl.splits * (size_t)(64 * pl.rt) * 128 * 4 : 0;
+}
+// p.x is the repacked copy of the activations (launch_repack_x; p.ldx unused)
+int launch_prefill_tall(const PrefillParams& p, const TallPlan& plan, int max_bits, int dtype, bool dense,
+                        hipStream_t st);
+// x [M][ldx] into the A-fragment order the kernel reads (tall_x_bytes bytes)
+size_t tall_x_bytes(int64_t M, int64_t K);
+int launch_repack_x(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* xt, hipStream_t st);
 
 // Large-batch fp16 prefill without the library path (prefill_wide.hip):
 // 256 x 256 output tiles, the weight dequantized into LDS per 64-row stage.

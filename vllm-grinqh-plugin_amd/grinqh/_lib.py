@@ -57,7 +57,30 @@ SIGNATURES = {
     "grinqh_gemv_batch_union_sigma": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _i32, _f4,
                                              _vp, _vp, ctypes.c_size_t, _vp]),
     "grinqh_time_next_product": (_i32, [_vp, _vp]),
+    "grinqh_product_kernel": (_i32, [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                     ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
 }
+
+KERNEL_GEMV = 1
+KERNEL_DECODE = 2
+KERNEL_TALL = 3
+KERNEL_LIBRARY = 4
+KERNEL_FUSED = 5
+KERNEL_NAMES = {KERNEL_GEMV: "gemv_kernel", KERNEL_DECODE: "decode_kernel", KERNEL_TALL: "prefill_tall_kernel",
+                KERNEL_LIBRARY: "dequant_nk_kernel + library GEMM", KERNEL_FUSED: "prefill_kernel"}
+
+
+def product_kernel(M: int, K: int, ldx: int, N: int, dtype: int, max_bits: int, group_size: int, mode: int,
+                   noalloc: bool = False):
+    """(kernel id, rows per block, K ranges of the split tiles) of the kernel
+    that serves such a product (grinqh_product_kernel); nothing is launched."""
+    lib = load_library()
+    rows, sp = _i32(0), _i32(0)
+    k = lib.grinqh_product_kernel(M, K, ldx, N, dtype, max_bits, group_size, mode, int(bool(noalloc)),
+                                  ctypes.byref(rows), ctypes.byref(sp))
+    if k < 0:
+        check(-k, "grinqh_product_kernel")
+    return k, rows.value, sp.value
 
 _lock = threading.Lock()
 _lib = None
