@@ -24,6 +24,27 @@ def to_dtype_np(a: np.ndarray, dtype: str) -> np.ndarray:
     return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(TORCH_DTYPES[dtype]).double().numpy()
 
 
+def rounds_weight(M: int, dtype: str = "float16") -> bool:
+    """Whether the kernel serving an M-row batch rounds w_eff*s to the
+    activation dtype (as the reference's dense path does, grinqh/kernel.py:586)
+    instead of applying the scale in fp32 after the sum: the prefill kernels
+    above 64 rows, and the fp16 decode kernel for 17-64 rows."""
+    return M > 64 or (M > 16 and dtype == "float16")
+
+
+def own_product(x, W, s, t, b, gs, dtype, graded):
+    """Float64 product the kernel serving this batch computes: S10 (graded) or
+    the exact dense product when it applies the scale after the sum, the same
+    with RNE(w_eff*s) -- S9 for the dense dispatch -- when it rounds the
+    scaled weight first.  Kernels are held to it with the base tolerance."""
+    from oracle import grinqh_oracle as O
+    M = np.asarray(x).reshape(-1, W.shape[0]).shape[0]
+    if rounds_weight(M, dtype):
+        return (O.gemv_union_rounded_f64(x, W, s, t, b, gs, dtype) if graded
+                else O.dense_prefill_f64(x, W, s, gs, dtype))
+    return O.gemv_union_f64(x, W, s, t, b, gs) if graded else O.dense_exact_f64(x, W, s, gs)
+
+
 def dense_rounding_bound(x: np.ndarray, W: np.ndarray, scale: np.ndarray, dtype: str, group_size: int = 128):
     """Largest difference the reference's own elementwise rounding of W*s to
     the activation dtype (grinqh/kernel.py:586) can make to a dense product:

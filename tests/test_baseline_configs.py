@@ -34,7 +34,7 @@ import pytest
 import torch
 
 from oracle import grinqh_oracle as O
-from tests._helpers import UNIT_ROUNDOFF, assert_output_close, error_stats, record_errors
+from tests._helpers import UNIT_ROUNDOFF, assert_output_close, error_stats, record_errors, rounds_weight
 
 pytestmark = pytest.mark.gpu
 
@@ -51,13 +51,6 @@ def _gpu():
         pytest.fail("GPU tests need a HIP device")
     from grinqh import _lib
     _lib.load_library()
-
-
-def rounds_weight(M, dtype="float16"):
-    """Whether the kernel serving an M-row batch multiplies RNE(w_eff * s)
-    (the prefill kernels above 64 rows, the fp16 decode kernel for 17-64
-    rows) rather than applying the scale after the sum."""
-    return M > 64 or (M > 16 and dtype == "float16")
 
 
 _weights = {}

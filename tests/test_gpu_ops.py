@@ -14,7 +14,7 @@ import torch
 
 from oracle import grinqh_oracle as O
 from tests._helpers import (TORCH_DTYPES, assert_output_close, dense_rounding_bound, error_stats,
-                            rand_weight, record_errors, to_dtype_np)
+                            own_product, rand_weight, record_errors, rounds_weight, to_dtype_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -44,26 +44,6 @@ def _setup(rng, K, N, b, dtype, M=1, scale_sd=1.0):
 def _prepare(W, b):
     from grinqh.utils import prepare_weight
     return prepare_weight(_dev(W), b)
-
-
-def rounds_weight(M, dtype):
-    """Whether the kernel serving an M-row batch rounds w_eff*s to the
-    activation dtype (as the reference's dense path does, grinqh/kernel.py:586)
-    instead of applying the scale in fp32 after the sum: the prefill kernels
-    above 64 rows, and the fp16 decode kernel for 17-64 rows."""
-    return M > 64 or (M > 16 and dtype == "float16")
-
-
-def own_product(x, W, s, t, b, gs, dtype, graded):
-    """Float64 product the kernel serving this batch computes: S10 (graded) or
-    the exact dense product when it applies the scale after the sum, the same
-    with RNE(w_eff*s) -- S9 for the dense dispatch -- when it rounds the
-    scaled weight first.  Kernels are held to it with the base tolerance."""
-    M = np.asarray(x).reshape(-1, W.shape[0]).shape[0]
-    if rounds_weight(M, dtype):
-        return (O.gemv_union_rounded_f64(x, W, s, t, b, gs, dtype) if graded
-                else O.dense_prefill_f64(x, W, s, gs, dtype))
-    return O.gemv_union_f64(x, W, s, t, b, gs) if graded else O.dense_exact_f64(x, W, s, gs)
 
 
 def _tdt(x, dtype):
