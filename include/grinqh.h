@@ -167,10 +167,19 @@ int grinqh_gemv_batch_union_sigma(const void* x, int64_t M, int64_t K, int64_t l
  * arguments, semantics and results as grinqh_gemm_or_gemv, without the
  * workspace: its split-K counters, partial sums and grading statistic live in
  * a fixed device array of GRINQH_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU
- * holds from the first call until the process ends.  It calls no allocator.
- * Every batch size runs on the fused kernels (the library-GEMM prefill path,
- * which needs a 2*N*K dense weight buffer, is not taken), and a product whose
- * scratch would exceed the array returns GRINQH_ERR_SCRATCH.  All calls on one
+ * holds from the first call until the process ends.  It calls no allocator
+ * of its own (no hipMalloc, hipFree or allocating library routine).  A few
+ * kernel instantiations spill registers to the private-segment (scratch)
+ * memory that the HIP runtime sets up for a device's queues (the large-batch
+ * kernel's 512-row blocks, the 33-64-row decode kernel: tests check the
+ * build's resource report); a caller that must see no runtime allocation at
+ * all runs one call of each shape class first.  The library-GEMM prefill path
+ * (a 2*N*K dense weight buffer) is not taken: from 256 rows the hand-written
+ * large-batch kernel runs where its repacked activations fit the array, else
+ * the fused kernels; a decode batch whose split-K partial sums would outgrow
+ * the array runs in row chunks graded on the whole batch's statistic.  A
+ * product that still does not fit (a fused prefill with many K ranges)
+ * returns GRINQH_ERR_SCRATCH.  All calls on one
  * GPU share the array, so calls that overlap in time on one GPU (different
  * streams, or several threads) race; calls ordered on one stream do not.
  * The device current in the calling thread must be the one that holds the

@@ -6,10 +6,11 @@ time with a smaller batch (the scratch array keeps the first call's contents:
 counters must be back at zero, partial sums must not leak), and checks both
 results bitwise against grinqh_gemm_or_gemv on the same inputs: the GEMV
 (one and four rows), the decode kernel (graded and dense), the fused prefill
-(graded, dense, and split over K).  From 512 rows (and from 257 with
-K <= 8192) the workspace entry point takes the library GEMM while the
-allocation-free one keeps the fused kernels, so that case is held to the
-oracle instead.
+(graded, dense, and split over K).  Where the workspace entry point takes
+the library GEMM the allocation-free one runs the hand-written large-batch
+kernel, and where a decode launch's split-K partial sums outgrow the fixed
+scratch it runs the rows in chunks: those cases are held to the oracle
+instead.
 """
 import ctypes
 
@@ -87,10 +88,10 @@ def test_noalloc_matches_workspace_entry_point(lib, K, N, mode, m1, m2):
         assert torch.equal(got, want), f"M={M}: max |diff| {(got.float() - want.float()).abs().max().item()}"
 
 
-def test_noalloc_large_batch_stays_on_fused_kernel(lib):
-    """512 rows: the allocation-free entry point runs the fused prefill (no
-    dense weight buffer); it computes S9 (RNE(w*s), the dense dispatch) and
-    is held to the oracle."""
+def test_noalloc_large_batch_without_library(lib):
+    """512 rows: the allocation-free entry point runs the hand-written
+    large-batch kernel (no dense weight buffer); it computes S9 (RNE(w*s), the
+    dense dispatch) and is held to the oracle."""
     from grinqh.utils import prepare_weight
     rng = np.random.default_rng(3)
     M, K, N = 512, 1024, 2048
@@ -100,3 +101,39 @@ def test_noalloc_large_batch_stays_on_fused_kernel(lib):
     pre = O.dense_prefill_f64(x, W, s, 128, "float16")
     assert_output_close(y, pre, O.dense_prefill(x, W, s, b, 128, "float16"), "float16", bias=b,
                         what="noalloc 512-row prefill")
+
+
+@pytest.mark.parametrize("M", [40, 64])
+def test_noalloc_large_k_decode_runs_in_row_chunks(lib, M):
+    """Llama-3-405B down_proj (K = 53248, N = 16384): a decode launch of M
+    rows needs at least 26 K ranges of M x N fp32 partial sums (68 MiB at 40
+    rows, 104 MiB at 64), more than the 64 MiB scratch.  The allocation-free
+    entry point then runs the rows in chunks that fit, graded on the whole
+    batch's statistic (reduced once into the scratch), and the result is held
+    to the oracle (32-row chunks, like 40 and 64 rows, take the rounded scaled
+    weight) on a slice of the columns, twice in a row; a following small call
+    shows the counters are back at zero."""
+    from grinqh.utils import prepare_weight
+    K, N = 53248, 16384
+    rng = np.random.default_rng(405)
+    W = rng.integers(-128, 128, size=(K, N), dtype=np.int8)
+    x = to_dtype_np(rng.standard_normal((M, K)), "float16")
+    s = to_dtype_np(rng.standard_normal((K // 128, N)) * 0.02, "float16")
+    P = prepare_weight(torch.from_numpy(W).cuda(), 8)
+    st = _dev(s)
+    sigma = np.abs(x).max(0).astype(np.float32)
+    t = [0.0] + np.quantile(sigma, [0.5, 0.8, 0.95]).tolist()
+    cols = np.r_[0:256, N - 256:N]
+    pre = O.gemv_union_rounded_f64(x, W[:, cols], s[:, cols], t, 8, 128, "float16")
+    fin = O.bias_add(pre, None, "float16")
+    xt = _dev(x)
+    for _ in range(2):
+        y = _noalloc(lib, xt, P, st, None, N, t, "union")
+        assert_output_close(y[:, torch.from_numpy(cols).cuda()], pre, fin, "float16",
+                            what=f"noalloc 405B down_proj M={M}")
+    # a small call after: the split-K counters the chunks used are zero again
+    xs = _dev(x[:4])
+    pre4 = O.gemv_union_f64(x[:4], W[:, cols], s[:, cols], t, 8, 128)
+    y4 = _noalloc(lib, xs, P, st, None, N, t, "union")
+    assert_output_close(y4[:, torch.from_numpy(cols).cuda()], pre4, O.bias_add(pre4, None, "float16"), "float16",
+                        what="noalloc 405B down_proj M=4 after the chunked call")

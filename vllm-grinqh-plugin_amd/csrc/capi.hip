@@ -320,8 +320,30 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   const bool graded = mode == GRINQH_MODE_UNION || (mode == GRINQH_MODE_REFERENCE && M == 1);
   if (graded && thresholds == nullptr) return GRINQH_ERR_INVALID;
 
-  const WorkspaceLayout wl = layout_for(M, K, N, graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE, allow_library,
-                                        ldx, group_size, allow_library ? 0 : ws_bytes);
+  const int mode_l = graded ? GRINQH_MODE_UNION : GRINQH_MODE_DENSE;
+  WorkspaceLayout wl = layout_for(M, K, N, mode_l, allow_library, ldx, group_size, allow_library ? 0 : ws_bytes);
+  // The allocation-free entry point's fixed scratch may not hold a decode
+  // launch's split-K partial sums (a large K forces many K ranges, and the
+  // partial sums grow with the rows): then the rows run in chunks (halving
+  // until one chunk's layout fits), graded on the statistic of the whole
+  // batch, reduced once into the scratch past the chunks' layout.  With one
+  // row every valid shape fits.
+  int64_t rows_per_launch = kDecodeMaxRows;
+  size_t sigma_off = 0;
+  if (!allow_library && M <= kDecodeMaxRows && wl.total > ws_bytes) {
+    const size_t sig_bytes = graded && sigma_given == nullptr ? round_up((size_t)K * sizeof(float), 256) : 0;
+    auto need = [&](const WorkspaceLayout& w) {
+      return round_up(w.total > kCounterBytes ? w.total : kCounterBytes, 256) + sig_bytes;
+    };
+    int64_t mc = M;
+    while (mc > 1 && need(wl) > ws_bytes) {
+      mc = (mc + 1) / 2;
+      wl = layout_for(mc, K, N, mode_l, false, ldx, group_size, ws_bytes);
+    }
+    if (need(wl) > ws_bytes) return GRINQH_ERR_SCRATCH;
+    rows_per_launch = mc;
+    sigma_off = need(wl) - sig_bytes;
+  }
   if (wl.total > 0 && (workspace == nullptr || ws_bytes < wl.total || !aligned(workspace, 256)))
     return allow_library ? GRINQH_ERR_WORKSPACE : GRINQH_ERR_SCRATCH;
   hipStream_t st = as_stream(stream);
@@ -346,9 +368,15 @@ int run_product(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t N, int
   if (graded && sigma_given != nullptr) {  // the producer's chunk maxima (grinqh_*_sigma)
     p.sigma = sigma_given;
     p.sigma_chunks = (int)((M + kSigmaChunkRows - 1) / kSigmaChunkRows);
+  } else if (graded && rows_per_launch < M) {  // row chunks: grade on the whole batch's statistic
+    float* sig = reinterpret_cast<float*>(ws + sigma_off);
+    rc = launch_sigma(xs, ldx, (int)M, (int)K, dtype, sig, st);
+    if (rc != GRINQH_OK) return rc;
+    p.sigma = sig;
+    p.sigma_chunks = 1;
   }  // else the GEMV and decode kernels reduce the batch statistic of their rows themselves
-  for (int64_t m0 = 0; m0 < M; m0 += kDecodeMaxRows) {
-    const int64_t mc = (M - m0) < kDecodeMaxRows ? (M - m0) : kDecodeMaxRows;
+  for (int64_t m0 = 0; m0 < M; m0 += rows_per_launch) {
+    const int64_t mc = (M - m0) < rows_per_launch ? (M - m0) : rows_per_launch;
     const DecodePlan plan = plan_launch(mc, K, N, group_size);
     p.x = xs + m0 * ldx;
     p.y = ys + m0 * N;

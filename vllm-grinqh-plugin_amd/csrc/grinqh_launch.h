@@ -118,7 +118,6 @@ int prefill_splits(int64_t M, int64_t K, int64_t N);
 // filled round) split K into `splits` ranges, completed in the kernel
 // (partial sums, per-tile counters).
 constexpr int64_t kTallPrefillRows = 256;
-constexpr int kTallDoneBase = kMaxCounters / 2;  // counters: arrivals [0, 2048), done [2048, 4096)
 struct TallPlan {
   int rt;        // 16-row tiles per wave: 8 (512-row blocks) or 4 (256-row blocks)
   int splits;    // K ranges of the split tiles

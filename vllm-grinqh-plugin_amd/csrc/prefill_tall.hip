@@ -417,16 +417,15 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   auto value = [&](int i, int tt, int v) {
     return DENSE ? acc[i][tt][v] : graded_nonfinite_to_nan(acc[i][tt][v] * up_scale);
   };
-  int64_t ncol[8];
-#pragma unroll
-  for (int tt = 0; tt < 8; ++tt) ncol[tt] = (int64_t)(2 * tt + (kq >> 1)) * p.NW + w0 + 4 * (kq & 1);
-  auto elem = [&](int i, int tt) -> int64_t { return (int64_t)(row0 + 16 * i + l16) * p.N + ncol[tt]; };
+  // (columns computed per tile, 32-bit: N < 2^24; the row offset in 64 bits)
+  const int ncol0 = (kq >> 1) * p.NW + w0 + 4 * (kq & 1);
+  auto ncol = [&](int tt) { return ncol0 + 2 * tt * p.NW; };
+  auto elem = [&](int i, int tt) -> int64_t { return (int64_t)(row0 + 16 * i + l16) * p.N + ncol(tt); };
   auto out4 = [&](int i, int tt, f32x4_t a) {  // four outputs of one row: one 8-byte store
+    const int n = ncol(tt);
     u32x2_t h;
-    h[0] = (uint32_t)finish_output<DT>(a[0], p.bias, (int)ncol[tt]) |
-           ((uint32_t)finish_output<DT>(a[1], p.bias, (int)ncol[tt] + 1) << 16);
-    h[1] = (uint32_t)finish_output<DT>(a[2], p.bias, (int)ncol[tt] + 2) |
-           ((uint32_t)finish_output<DT>(a[3], p.bias, (int)ncol[tt] + 3) << 16);
+    h[0] = (uint32_t)finish_output<DT>(a[0], p.bias, n) | ((uint32_t)finish_output<DT>(a[1], p.bias, n + 1) << 16);
+    h[1] = (uint32_t)finish_output<DT>(a[2], p.bias, n + 2) | ((uint32_t)finish_output<DT>(a[3], p.bias, n + 3) << 16);
     *reinterpret_cast<u32x2_t*>(&p.y[elem(i, tt)]) = h;
   };
   if (splits == 1) {  // tile by tile (the barrier keeps the accumulator reads from being hoisted)
@@ -440,47 +439,34 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
       }
     return;
   }
-  // split over K: the ranges of a tile count their arrival on the tile's
-  // counter.  All but the last store their partial sums (16-byte agent-scope
-  // stores, written through L2; lane-major, one contiguous KiB per store) and
-  // then count themselves done; the last waits for them -- they arrived
-  // before it, so they are running and finish without waiting on anything --
-  // and adds all ranges in range order 0, 1, ..., its own from registers, so
-  // the result does not depend on which range arrived last.  It then clears
-  // both counters for the next launch.
+  // split over K: every range stores its partial sums (16-byte agent-scope
+  // stores, written through L2; lane-major, one contiguous KiB per store) and,
+  // once they have completed, counts itself done on the tile's counter; the
+  // range that counts last reads all ranges back and adds them in range order
+  // 0, 1, ..., so the result does not depend on which range finished last,
+  // then clears the counter for the next launch.  Its accumulators are free
+  // by then, which keeps the reduction's registers apart from them.
   constexpr uint32_t kTileBytes = (uint32_t)BM * 128u * 4u;
   const uint32_t part_bytes = (uint32_t)((gridDim.x - (unsigned)p.dp_tiles) / (unsigned)p.splits) *
                               (uint32_t)p.splits * kTileBytes;  // below 2^31: the partial area is capped
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.partial, (short)0, (int)part_bytes, 0x00020000);
   auto poff = [&](int i, int tt) { return (uint32_t)(((wave * RT + i) * 8 + tt) * 1024 + lane * 16); };
   auto range_base = [&](int sp) { return (uint32_t)(jt * p.splits + sp) * kTileBytes; };
-  __shared__ int s_order;
-  if (tid == 0) s_order = (int)atomicAdd(&p.counters[jt], 1u);
-  __syncthreads();
-  if (s_order != splits - 1) {
 #pragma unroll
-    for (int i = 0; i < RT; ++i)
+  for (int i = 0; i < RT; ++i)
 #pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const f32x4_t v{value(i, tt, 0), value(i, tt, 1), value(i, tt, 2), value(i, tt, 3)};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, (int)poff(i, tt),
-                                               (int)range_base(split), kCpolSc1);
-      }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
-    __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(&p.counters[kTallDoneBase + jt], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  if (tid == 0) {
-    // bounded: the ranges waited for are running and wait on nothing
-    for (uint32_t n = 0; n < (1u << 22) && __hip_atomic_load(&p.counters[kTallDoneBase + jt], __ATOMIC_ACQUIRE,
-                                                              __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)(splits - 1);
-         ++n)
-      __builtin_amdgcn_s_sleep(2);
-  }
+    for (int tt = 0; tt < 8; ++tt) {
+      const f32x4_t v{value(i, tt, 0), value(i, tt, 1), value(i, tt, 2), value(i, tt, 3)};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), prs, (int)poff(i, tt),
+                                             (int)range_base(split), kCpolSc1);
+    }
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
   __syncthreads();
-  auto term = [&](int sp, int i, int tt) -> f32x4_t {  // range sp's sums of one row of a 16 x 16 tile
-    if (sp == split) return f32x4_t{value(i, tt, 0), value(i, tt, 1), value(i, tt, 2), value(i, tt, 3)};
+  if (tid == 0) s_last = atomicAdd(&p.counters[jt], 1u) == (unsigned)(splits - 1);
+  __syncthreads();
+  if (!s_last) return;
+  auto load = [&](int sp, int i, int tt) {  // range sp's sums of one row of a 16 x 16 tile
     return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)poff(i, tt),
                                                                               (int)range_base(sp), kCpolSc1));
   };
@@ -489,11 +475,11 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   for (int i = 0; i < RT; ++i) {
     f32x4_t sum[8];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) sum[tt] = term(0, i, tt);
+    for (int tt = 0; tt < 8; ++tt) sum[tt] = load(0, i, tt);
     for (int sp = 1; sp < splits; ++sp) {
       f32x4_t v[8];
 #pragma unroll
-      for (int tt = 0; tt < 8; ++tt) v[tt] = term(sp, i, tt);
+      for (int tt = 0; tt < 8; ++tt) v[tt] = load(sp, i, tt);
 #pragma unroll
       for (int tt = 0; tt < 8; ++tt) sum[tt] += v[tt];
     }
@@ -507,11 +493,9 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
         out4(i, tt, sum[tt]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (tid == 0) {  // atomic (agent scope) like every other access: a plain store may wait in this XCD's L2
-    __hip_atomic_store(&p.counters[jt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&p.counters[kTallDoneBase + jt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (tid == 0) __hip_atomic_store(&p.counters[jt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------------ x repack
@@ -580,7 +564,7 @@ TallPlan plan_tall(int64_t M, int64_t K, int64_t N, size_t max_partial) {
     consider(1, tiles, (double)((tiles + slots - 1) / slots) * (double)stages * f);
     for (int64_t dp : {tiles / slots * slots, (int64_t)0}) {
       const int64_t tail = tiles - dp;
-      if (tail == 0 || tail > kTallDoneBase) continue;
+      if (tail == 0 || tail > kMaxCounters) continue;
       for (int s = 2; s <= 4; ++s) {
         const size_t part = (size_t)tail * (size_t)s * (size_t)rows * 128 * 4;
         if (stages / s < 8 || part > max_partial) continue;
@@ -626,7 +610,7 @@ int launch_prefill_tall(const PrefillParams& p, const TallPlan& plan, int max_bi
   const int64_t rows = 64 * plan.rt;
   const int64_t tiles = ((p.M + rows - 1) / rows) * (p.NW / kTallWords);
   if (plan.tiles != tiles || p.dp_tiles < 0 || p.dp_tiles > tiles || (p.splits == 1) != (p.dp_tiles == tiles) ||
-      tiles - p.dp_tiles > kTallDoneBase)
+      tiles - p.dp_tiles > kMaxCounters)
     return GRINQH_ERR_INVALID;
   if (p.splits > 1 && (p.partial == nullptr || p.counters == nullptr)) return GRINQH_ERR_INVALID;
   const int Z = max_bits / 2;
