@@ -20,7 +20,7 @@ per-case product times, the roofline of the dominant kernel, the prefill
 TFLOP/s at M=2048 (dense, the reference's dispatch for M > 1), the graded
 prefill sweep of BASELINE configs[2] (M = 512, 2048, 8192, 70/20/8/2 % grade
 mix), the M=2048 products without the library path (allocation-free entry
-point: the hand-written wide-tile kernel instead of the dense weight and the
+point: the hand-written large-batch kernel instead of the dense weight and the
 library GEMM), the Llama-3-70B shapes of BASELINE configs[4] with every zone
 active (M = 1, 64, 4096) and the CPU baseline (the reference's pure-PyTorch
 math on the host cores).
@@ -97,9 +97,9 @@ def prefill_kernel_name(M, K, N, mode, noalloc=False):
 
 def library_free_product(torch, lib, x, P, s, t, mode):
     """One product through grinqh_gemm_or_gemv_noalloc (include/grinqh.h): no
-    workspace, so no dense weight for the library GEMM; fp16 batches of 512
-    rows and more run the wide-tile prefill kernel where its grid fills the
-    GPU, else the fused prefill kernel."""
+    workspace, so no dense weight for the library GEMM; batches of 256 rows
+    and more run the hand-written large-batch kernel (prefill_tall_kernel)
+    where its shape rules allow, else the fused prefill kernel."""
     from grinqh import _lib
     M, K = x.shape
     N = s.shape[1]

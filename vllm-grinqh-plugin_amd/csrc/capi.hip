@@ -182,9 +182,10 @@ int check_product_args(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t
 // larger activations.
 bool x_fits_fused_prefill(int64_t M, int64_t ldx) { return M * ldx * 2 < ((int64_t)1 << 31); }
 
-// M > kDecodeMaxRows: the library-GEMM path (use_library_gemm, when the
-// library has an algorithm without workspace for the shape), else one prefill
-// launch over the whole batch, the wide-tile kernel where it applies
+// M > kDecodeMaxRows: the large-batch kernel where the layout chose it
+// (wl.tall), else the library-GEMM path (use_library_gemm, when the library
+// has an algorithm without workspace for the shape), else one prefill launch
+// over the whole batch, the wide-tile kernel where it applies
 // (prefill_wide_applies) or the fused prefill kernel (graded batches first
 // reduce the union statistic over all M rows).  The workspace layout holds
 // the fused kernel's regions in front of the library path's, so either runs.
@@ -263,7 +264,7 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     return rc;
   }
   if (!x_fits_fused_prefill(M, d.ldx)) return GRINQH_ERR_INVALID;  // x of 2 GiB or more: split the batch
-  // without the library path (allocation-free entry point): the wide-tile
+  // neither the large-batch kernel nor the library path: the wide-tile
   // kernel where its grid fills the GPU, else the fused prefill kernel
   const bool wide = prefill_wide_applies(M, d.K, d.N, d.ldx, d.gs, dtype);
   PrefillParams p{};
