@@ -267,13 +267,14 @@ def test_tall_nonfinite_rows(lib, splits_wanted):
 @pytest.mark.parametrize("mode", ["dense", "union"])
 def test_tall_gate_up_2048(lib, mode):
     """Llama-3-8B gate_up (K = 4096, N = 28672) at 2048 rows, the configs[2]
-    point the bench times: 512-row blocks, 896 tiles of 512 x 128, the
-    first 768 (three full rounds) with K in one range, the last 128 (word
-    columns 1536..1791) in two; the first and last 64 rows held to the oracle
-    on a slice of the columns that holds both kinds, the graded zone sets
-    from the whole batch's statistic.  The allocation-free entry point has no
-    room for the partial sums and runs every tile whole: held to the oracle
-    too, and equal bit for bit where the workspace call ran whole tiles."""
+    point the bench times: 512-row blocks, 896 tiles of 512 x 128 in row
+    block order (224 column blocks each), the first 768 (three full rounds)
+    with K in one range, the last 128 (row block 3, word columns 768..1791)
+    in two; the first and last 64 rows held to the oracle on a slice of the
+    columns that holds both kinds, the graded zone sets from the whole
+    batch's statistic.  The allocation-free entry point has no room for the
+    partial sums and runs every tile whole: held to the oracle too, and equal
+    bit for bit where the workspace call ran whole tiles."""
     from grinqh import _lib
     rng = np.random.default_rng(6900)
     M, K, N, b = 2048, 4096, 28672, 8
@@ -299,5 +300,6 @@ def test_tall_gate_up_2048(lib, mode):
     yn = _noalloc(lib, xt, P, st, None, N, b, t, mode)
     assert_output_close(yn[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()], pre, fin, "float16",
                         what=f"tall prefill gate_up 2048 {mode} without workspace")
-    whole = torch.from_numpy(np.flatnonzero(np.arange(N) % (N // 16) < 1536)).cuda()
-    assert torch.equal(yn[:, whole], y[:, whole])
+    assert torch.equal(yn[:1536], y[:1536])  # row blocks 0-2: whole tiles
+    whole = torch.from_numpy(np.flatnonzero(np.arange(N) % (N // 16) < 768)).cuda()
+    assert torch.equal(yn[1536:, whole], y[1536:, whole])  # row block 3, column blocks 0-95
