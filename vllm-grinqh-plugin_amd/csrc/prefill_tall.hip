@@ -548,10 +548,16 @@ bool prefill_tall_applies(int64_t M, int64_t K, int64_t N, int64_t ldx, int gs) 
 // as few rounds of as few stages as possible.  Whole tiles fill full rounds
 // (dp_tiles); the tiles left over (or all of them) split K into 2..4 ranges,
 // so that the last round is shorter instead of partly empty.  Cost in units
-// of one 512-row block's stage: rounds * stages per item * (1 for RT = 8,
-// 0.62 for RT = 4: half the MFMAs, the same dequantization), plus the
-// partial sums of the split tiles (written by all ranges but one, read once)
-// at about 9 MB per unit.
+// of one 512-row block's stage: rounds * stages per item * (1 for RT = 8;
+// for RT = 4, half the MFMAs and the same dequantization, 0.62 when the
+// launch is one round and 0.85 over several), plus the partial sums of the
+// split tiles (written by all ranges but one, read once) at about 9 MB per
+// unit.  The two RT = 4 factors are fitted to kernel times (MI355X, dense
+// fp16): one round, 0.6-0.7 (qkv at 512 rows: 50 us against 60 us for
+// 512-row blocks in four K ranges; o_proj at 1024: 55 against 65 us);
+// several rounds, 0.85-0.89 (gate_up at 768 rows: 323 us in 256-row blocks
+// over 2 rounds and a 3-way split tail, 266 us in 512-row blocks; qkv at
+// 2048: 172 against 124 us).
 TallPlan plan_tall(int64_t M, int64_t K, int64_t N, size_t max_partial) {
   const int64_t stages = K / kTallBK;
   const int64_t col_blocks = (N / 16) / kTallWords;
@@ -561,23 +567,27 @@ TallPlan plan_tall(int64_t M, int64_t K, int64_t N, size_t max_partial) {
   for (int rt : {8, 4}) {
     const int64_t rows = 64 * rt;
     const int64_t tiles = ((M + rows - 1) / rows) * col_blocks;
-    const double f = rt == 4 ? 0.62 : 1.0;
+    auto f = [rt](int64_t rounds) { return rt == 8 ? 1.0 : rounds <= 1 ? 0.62 : 0.85; };
     auto consider = [&](int s, int64_t dp, double cost) {
       if (cost < best_cost - 1e-9) {
         best_cost = cost;
         best = TallPlan{rt, s, (int)dp, (int)tiles};
       }
     };
-    consider(1, tiles, (double)((tiles + slots - 1) / slots) * (double)stages * f);
+    const int64_t rounds_whole = (tiles + slots - 1) / slots;
+    consider(1, tiles, (double)rounds_whole * (double)stages * f(rounds_whole));
     for (int64_t dp : {tiles / slots * slots, (int64_t)0}) {
       const int64_t tail = tiles - dp;
       if (tail == 0 || tail > kMaxCounters) continue;
       for (int s = 2; s <= 4; ++s) {
         const size_t part = (size_t)tail * (size_t)s * (size_t)rows * 128 * 4;
         if (stages / s < 8 || part > max_partial) continue;
-        const double rounds_dp = (double)(dp / slots), rounds_tail = (double)((tail * s + slots - 1) / slots);
+        const int64_t rounds_dp = dp / slots, rounds_tail = (tail * s + slots - 1) / slots;
         const double traffic = (double)tail * (double)(s - 1) * (double)rows * 128.0 * 4.0 * 2.0 / 9.0e6;
-        consider(s, dp, (rounds_dp * (double)stages + rounds_tail * (double)((stages + s - 1) / s)) * f + traffic);
+        consider(s, dp,
+                 ((double)rounds_dp * (double)stages + (double)rounds_tail * (double)((stages + s - 1) / s)) *
+                         f(rounds_dp + rounds_tail) +
+                     traffic);
       }
     }
   }
