@@ -273,18 +273,22 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   int up_exp = 0;  // the block's sums are scaled by 2^up_exp at the end
   // The scales into LDS, once the first tiles' plane loads are issued; then
   // the overflow guard.  The barriers carry no memory fence, so they do not
-  // wait for those plane loads, only for the LDS accesses before them.
+  // wait for those plane loads, only for the LDS accesses before them.  One
+  // staging path per block: where the 16-byte loads were not issued their
+  // zero fill would race with the element-wise stores to the same LDS words.
   auto stage_scales = [&]() {
+    if (vec_scales) {
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      const int h = tid + NT * k;
-      if ((h >> 5) < SC_GROUPS) *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
-      if constexpr (GUARD) {
+      for (int k = 0; k < SPT; ++k) {
+        const int h = tid + NT * k;
+        if ((h >> 5) < SC_GROUPS)
+          *reinterpret_cast<u32x4_t*>(&s_scale[(h >> 5) * 256 + ((h >> 1) & 15) * 16 + 8 * (h & 1)]) = sv[k];
+        if constexpr (GUARD) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) smax = max(smax, max(sv[k][e] & 0x7FFFu, (sv[k][e] >> 16) & 0x7FFFu));
+          for (int e = 0; e < 4; ++e) smax = max(smax, max(sv[k][e] & 0x7FFFu, (sv[k][e] >> 16) & 0x7FFFu));
+        }
       }
-    }
-    if (!vec_scales) {  // column count not a multiple of 128: element-wise scale staging
+    } else {  // column count not a multiple of 128: element-wise scale staging
       for (int idx = tid; idx < n_groups * 256; idx += NT) {
         const int gl = idx >> 8, col = idx & 255;
         const int wcol = min(w0 + (col & 15), p.NW - 1);
@@ -712,10 +716,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // sigma_k = max_m |x[m][k]| over the whole batch (NaN ignored unless all NaN,
 // as fmaxf does), computed once for kernels that grade from it.  A block
 // covers 32 columns; its 8 row groups take every 8th row with 8 loads in
-// flight each, and the 8 partial maxima are combined through LDS.
-template <typename DT>
+// flight each, and the 8 partial maxima are combined through LDS.  GZ = 0
+// writes sigma; GZ = Z writes each row's grade word (grade_word) instead.
+template <typename DT, int GZ>
 __global__ __launch_bounds__(256) void sigma_kernel(const uint16_t* __restrict__ x, int64_t ldx, int M, int K,
-                                                    float* __restrict__ sigma) {
+                                                    float* __restrict__ sigma, uint32_t* __restrict__ grades,
+                                                    GradeThresholds thr) {
   constexpr int COLS = 32, GROUPS = 256 / COLS, BATCH = 8;
   __shared__ float s_part[GROUPS][COLS];
   const int kk = threadIdx.x % COLS, mg = threadIdx.x / COLS;
@@ -737,7 +743,10 @@ __global__ __launch_bounds__(256) void sigma_kernel(const uint16_t* __restrict__
   if (mg == 0 && k < K) {
 #pragma unroll
     for (int g = 1; g < GROUPS; ++g) s = fmaxf(s, s_part[g][kk]);
-    sigma[k] = s;
+    if constexpr (GZ == 0)
+      sigma[k] = s;
+    else
+      grades[k] = grade_word<DT, GZ>(s, thr.t);
   }
 }
 
@@ -848,10 +857,34 @@ int launch_splitk_reduce(const DecodeParams& p, int splits, int dtype, hipStream
 int launch_sigma(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* sigma, hipStream_t st) {
   if (K == 0) return GRINQH_OK;
   const dim3 grid((K + 31) / 32);
+  const GradeThresholds none{};
   if (dtype == GRINQH_DTYPE_BF16)
-    hipLaunchKernelGGL(sigma_kernel<BF16>, grid, dim3(256), 0, st, x, ldx, M, K, sigma);
+    hipLaunchKernelGGL((sigma_kernel<BF16, 0>), grid, dim3(256), 0, st, x, ldx, M, K, sigma, nullptr, none);
   else
-    hipLaunchKernelGGL(sigma_kernel<F16>, grid, dim3(256), 0, st, x, ldx, M, K, sigma);
+    hipLaunchKernelGGL((sigma_kernel<F16, 0>), grid, dim3(256), 0, st, x, ldx, M, K, sigma, nullptr, none);
+  return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
+}
+
+template <typename DT>
+static void launch_grade_words_dt(const uint16_t* x, int64_t ldx, int M, int K, int Z, const GradeThresholds& thr,
+                                  uint32_t* grades, hipStream_t st) {
+  const dim3 grid((K + 31) / 32);
+  switch (Z) {
+    case 1: hipLaunchKernelGGL((sigma_kernel<DT, 1>), grid, dim3(256), 0, st, x, ldx, M, K, nullptr, grades, thr); break;
+    case 2: hipLaunchKernelGGL((sigma_kernel<DT, 2>), grid, dim3(256), 0, st, x, ldx, M, K, nullptr, grades, thr); break;
+    case 3: hipLaunchKernelGGL((sigma_kernel<DT, 3>), grid, dim3(256), 0, st, x, ldx, M, K, nullptr, grades, thr); break;
+    default: hipLaunchKernelGGL((sigma_kernel<DT, 4>), grid, dim3(256), 0, st, x, ldx, M, K, nullptr, grades, thr); break;
+  }
+}
+
+int launch_grade_words(const uint16_t* x, int64_t ldx, int M, int K, int dtype, int max_bits,
+                       const GradeThresholds& thr, uint32_t* grades, hipStream_t st) {
+  if (K == 0) return GRINQH_OK;
+  if (max_bits < 2 || max_bits > 8 || (max_bits & 1)) return GRINQH_ERR_INVALID;
+  if (dtype == GRINQH_DTYPE_BF16)
+    launch_grade_words_dt<BF16>(x, ldx, M, K, max_bits / 2, thr, grades, st);
+  else
+    launch_grade_words_dt<F16>(x, ldx, M, K, max_bits / 2, thr, grades, st);
   return hipGetLastError() == hipSuccess ? GRINQH_OK : GRINQH_ERR_HIP;
 }
 

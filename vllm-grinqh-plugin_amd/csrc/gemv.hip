@@ -283,12 +283,15 @@ __global__ __launch_bounds__(256, gemv_blocks_per_cu(MR)) void gemv_kernel(Decod
     issue(t_begin + 1, DB);
     // the scales, now that the first tiles' loads are in flight; the barrier
     // does not wait for those loads (no memory fence), only for the LDS stores
+    // one of two staging paths per block: the 16-byte loads' zero fill (when
+    // they were not issued) would race with element-wise stores to the same words
+    if (vec_scales) {
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) {
-      const int h = tid + 256 * k;
-      if (h < SCH) *reinterpret_cast<u32x4_t*>(&s_scale[h * 8]) = sv[k];
-    }
-    if (!vec_scales) {  // element-wise staging
+      for (int k = 0; k < SPT; ++k) {
+        const int h = tid + 256 * k;
+        if (h < SCH) *reinterpret_cast<u32x4_t*>(&s_scale[h * 8]) = sv[k];
+      }
+    } else {  // element-wise staging
       for (int idx = tid; idx < n_groups * 1024; idx += 256) {
         const int gl = idx >> 10, r = (idx >> 6) & 15;
         const int wcol = min(w0 + (idx & 63), p.NW - 1);
