@@ -212,11 +212,11 @@ int run_prefill(const DecodeParams& d, const uint16_t* xs, uint16_t* ys, int64_t
     p.dp_tiles = wl.tall_plan.dp_tiles;
     p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wl.partial_off) : nullptr;
     p.counters = p.splits > 1 ? reinterpret_cast<uint32_t*>(ws + wl.counter_off) : nullptr;
-    if (graded) {
-      float* sigma = reinterpret_cast<float*>(ws + wl.sigma_off);
-      rc = launch_sigma(xs, d.ldx, (int)M, d.K, dtype, sigma, st);
+    if (graded) {  // each K row's grade word, in the statistic's region (K words)
+      uint32_t* grades = reinterpret_cast<uint32_t*>(ws + wl.sigma_off);
+      rc = launch_grade_words(xs, d.ldx, (int)M, d.K, dtype, max_bits, d.thr, grades, st);
       if (rc != GRINQH_OK) return rc;
-      p.sigma = sigma;
+      p.grades = grades;
     }
     arm_kernel_timing();
     rc = launch_prefill_tall(p, wl.tall_plan, max_bits, dtype, !graded, st);

@@ -178,6 +178,26 @@ __device__ __forceinline__ int midpoint_bias(uint32_t bits) {
   return beta;
 }
 
+// Grade word of one K row for kernels that dequantize whole rows of a graded
+// batch (the large-batch prefill): the zone set of sigma_k in bits 16 .. 16 +
+// Z - 1, and in the low half the row constant of the dequantization with
+// sh = 8 - 2 Z: for fp16 activations -(1024 + (128 >> sh) - beta) as fp16
+// (added to 1024 + (u >> sh)), for bf16 the integer c_row = 128 - beta * 2^sh
+// (subtracted from u).  The same zone set and midpoint bias as zone_bits /
+// midpoint_bias of sigma_k, computed once per row instead of once per block.
+template <typename DT, int Z>
+__device__ __forceinline__ uint32_t grade_word(float sigma_abs, const float* thr) {
+  constexpr int SH = 8 - 2 * Z;
+  const uint32_t bits = zone_bits<Z>(sigma_abs, thr);
+  const int beta = midpoint_bias<Z>(bits);
+  uint32_t lo;
+  if constexpr (DT::id == F16::id)
+    lo = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta));
+  else
+    lo = (uint32_t)(uint16_t)(int16_t)(128 - beta * (1 << SH));
+  return lo | (bits << 16);
+}
+
 // ---------------------------------------------------------------- unpack
 
 // Bit-field insert: bits of `a` where `m` is set, bits of `b` elsewhere, in the

@@ -78,6 +78,10 @@ constexpr int64_t kGemvMaxRows = 4;
 DecodePlan plan_gemv(int64_t M, int64_t K, int64_t N, int64_t group_size);
 int launch_gemv(const DecodeParams& p, const DecodePlan& plan, int max_bits, int dtype, bool dense, hipStream_t st);
 int launch_sigma(const uint16_t* x, int64_t ldx, int M, int K, int dtype, float* sigma, hipStream_t st);
+// The union statistic's grade word of every K row (grade_word: zone set and
+// dequantization row constant, for max_bits / 2 planes), K uint32 at grades
+int launch_grade_words(const uint16_t* x, int64_t ldx, int M, int K, int dtype, int max_bits,
+                       const GradeThresholds& thr, uint32_t* grades, hipStream_t st);
 
 struct PrefillParams {
   const uint16_t* x;
@@ -94,6 +98,7 @@ struct PrefillParams {
   float* partial;        // [splits][M][N] fp32 when splits > 1 (the reduce kernel follows)
   uint32_t* counters;    // tall kernel with splits > 1: per split tile, zero on entry
   int dp_tiles;          // tall kernel: tiles computed whole, before the split ones
+  const uint32_t* grades;  // tall kernel, graded: grade word of every K row (launch_grade_words)
 };
 
 // Prefill path (M > kDecodeMaxRows): dequantize-into-LDS MFMA GEMM.  p.splits

@@ -195,11 +195,11 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   }
   const float down_scale = __builtin_ldexpf(1.f, -up_exp), up_scale = __builtin_ldexpf(1.f, up_exp);
 
-  // ---- registers of one stage's weight loads (planes and statistic, loaded
-  // one stage ahead of their dequantization) and the scale of the stage two
-  // ahead on its way to the LDS ring s_scale
+  // ---- registers of one stage's weight loads (planes and, graded, the two
+  // rows' grade words, loaded one stage ahead of their dequantization) and the
+  // scale of the stage two ahead on its way to the LDS ring s_scale
   uint32_t D[2][Z];
-  f32x2_t sig;
+  u32x2_t gw;
   uint16_t sc_in = 0;
   auto load_planes = [&](int s) {
     const uint32_t k0 = (uint32_t)(s * BK);
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
       for (int z = 0; z < Z; ++z)
         D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
             prsrc, (int)p_voff, (int)((k0 + (uint32_t)e) * row_bytes + (uint32_t)z * p.NW * 4u), 0);
-    if constexpr (!DENSE) sig = *reinterpret_cast<const f32x2_t*>(p.sigma + k0 + 2 * rp0);
+    if constexpr (!DENSE) gw = *reinterpret_cast<const u32x2_t*>(p.grades + k0 + 2 * rp0);
   };
   auto load_scale = [&](int s) {
     // the division is done on the vector unit; readfirstlane keeps the offset
@@ -218,8 +218,14 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
     sc_in = __builtin_amdgcn_raw_buffer_load_b16(srsrc, (int)s_voff, soff, 0);
   };
   // every thread stores the scale it loaded: the threads of one (sr, wc)
-  // loaded the same element, and no branch splits the MFMA loop
-  auto store_scale = [&](int slot) { s_scale[slot][wc * 16 + sr] = sc_in; };
+  // loaded the same element, and no branch splits the MFMA loop.  The
+  // overflow guard's factor is applied here, once per scale (unconditionally:
+  // exact when up_exp == 0), rather than to every scale a producer reads.
+  auto store_scale = [&](int slot) {
+    uint16_t v = sc_in;
+    if constexpr (GUARD) v = from_f32<DT>(to_f32<DT>(v) * down_scale);
+    s_scale[slot][wc * 16 + sr] = v;
+  };
 
   // ---- dequantization of one stage: prep grades the rows, flips and rotates
   // the planes and rebuilds all code dwords (V, so the plane registers are
@@ -229,28 +235,30 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   uint32_t negc;  // fp16: (-c_row) of the pair's two rows
   f32x2_t cbf;    // bf16: c_row of the two rows
   uint32_t s2[8];  // this word column's 16 scales (tiles 2 q, 2 q + 1), as loaded
-  // prep in pieces: grade (zone masks, midpoint bias and its constants, the
-  // offset-binary flip and plane rotation), code dwords of each group of four
-  // column tiles, scales
+  // prep in pieces: grade (zone masks and the row constants, from the rows'
+  // grade words when graded; the offset-binary flip and plane rotation), code
+  // dwords of each group of four column tiles, scales
   auto prep_grade = [&]() {
-    int beta[2];
+    if constexpr (!DENSE) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint32_t bits = DENSE ? ((1u << Z) - 1u) : zone_bits<Z>(sig[e], p.thr.t);
-      beta[e] = DENSE ? 0 : midpoint_bias<Z>(bits);
-      if constexpr (!DENSE) {
+      for (int e = 0; e < 2; ++e)
 #pragma unroll
-        for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((bits >> z) & 1u);
-      }
+        for (int z = 0; z < Z; ++z) D[e][z] &= 0u - ((gw[e] >> (16 + z)) & 1u);
     }
     const uint32_t xm[2] = {0xAAAAAAAAu, 0xAAAAAAAAu};  // offset binary: u = int8(U & mask) + 128
     prepare_planes<Z, 2>(D, xm);
     if constexpr (IS_F16) {
-      const uint16_t c0 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[0]));
-      const uint16_t c1 = f32_to_f16_bits(-(float)(1024 + (128 >> SH) - beta[1]));
-      negc = (uint32_t)c0 | ((uint32_t)c1 << 16);
+      if constexpr (DENSE) {
+        const uint32_t c = f32_to_f16_bits(-(float)(1024 + (128 >> SH)));
+        negc = c | (c << 16);
+      } else {
+        negc = (gw[0] & 0xFFFFu) | (gw[1] << 16);
+      }
     } else {
-      cbf = f32x2_t{(float)(128 - beta[0] * (1 << SH)), (float)(128 - beta[1] * (1 << SH))};
+      if constexpr (DENSE)
+        cbf = f32x2_t{128.f, 128.f};
+      else
+        cbf = f32x2_t{(float)(int16_t)(gw[0] & 0xFFFFu), (float)(int16_t)(gw[1] & 0xFFFFu)};
     }
   };
   auto prep_code = [&](int j) { code_dwords<Z, 2>(D, j, V[j]); };
@@ -260,16 +268,6 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
       const u32x4_t sa = *reinterpret_cast<const u32x4_t*>(&s_scale[sslot][wc * 16 + 8 * c]);
 #pragma unroll
       for (int q = 0; q < 4; ++q) s2[4 * c + q] = sa[q];
-    }
-    if constexpr (GUARD) {
-      // unconditionally (exact when up_exp == 0): a branch here would split
-      // the MFMA loop into blocks
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint16_t lo = from_f32<DT>(to_f32<DT>((uint16_t)(s2[q] & 0xFFFFu)) * down_scale);
-        const uint16_t hi = from_f32<DT>(to_f32<DT>((uint16_t)(s2[q] >> 16)) * down_scale);
-        s2[q] = (uint32_t)lo | ((uint32_t)hi << 16);
-      }
     }
   };
   auto prep = [&](int sslot) {
@@ -619,7 +617,7 @@ static int launch_tall_rt(const PrefillParams& p, int Z, bool dense, hipStream_t
 
 int launch_prefill_tall(const PrefillParams& p, const TallPlan& plan, int max_bits, int dtype, bool dense,
                         hipStream_t st) {
-  if (!dense && p.sigma == nullptr) return GRINQH_ERR_INVALID;
+  if (!dense && p.grades == nullptr) return GRINQH_ERR_INVALID;
   if (!prefill_tall_applies(p.M, p.K, p.N, p.ldx, p.gs) || p.splits != plan.splits || p.splits < 1 ||
       p.dp_tiles != plan.dp_tiles)
     return GRINQH_ERR_INVALID;
