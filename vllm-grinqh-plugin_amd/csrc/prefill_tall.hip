@@ -47,7 +47,6 @@ namespace {
 
 constexpr int kTallBK = 64;         // K rows per stage
 constexpr int kTallWords = 8;       // plane-word columns per block (128 logical columns)
-constexpr int kTallGroupRows = 1;   // row blocks per group of the block order
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -105,14 +104,16 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   // ---- work item: blocks renumbered so that each XCD runs consecutive items
   // (shared weight columns and x rows meet in one L2); items below dp_tiles
   // are whole tiles, the rest the K ranges of the split tiles, range fastest.
-  // Tile order: groups of kTallGroupRows row blocks, row block fastest.
-  // With one row block per group the columns run fastest: the tiles an XCD
-  // runs at the same time read the same rows of x (one row block instead of
-  // four), which its L2 then serves, and each weight tile comes back for
-  // the other row blocks from the memory side.  Measured at 2048 rows
-  // (dense, kernel time): gate_up 532 -> 499 us, down 280 -> 267 us, qkv
-  // unchanged, against groups of four row blocks (the weight shared on one
-  // XCD).
+  // Tile order: groups of GR row blocks, row block fastest.  512-row blocks
+  // take one row block per group (the columns run fastest): the tiles an
+  // XCD runs at the same time read the same rows of x, which its L2 then
+  // serves, and each weight tile comes back for the other row blocks from
+  // the memory side; at 2048 rows (dense, kernel time) gate_up took 532 ->
+  // 499 us and down 280 -> 267 us against groups of four.  256-row blocks
+  // (half the x per row block) keep groups of four, the weight shared by four
+  // row blocks on one XCD: down at 2048 rows without a workspace (eight row
+  // blocks, weights cold) 308 us against 320-332 us with one per group.
+  constexpr int GR = RT == 8 ? 1 : 4;
   const int col_blocks = p.NW / kTallWords, row_blocks = (p.M + BM - 1) / BM;
   const int item = xcd_chunked(blockIdx.x, gridDim.x);
   const bool whole = item < p.dp_tiles;
@@ -120,10 +121,10 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
   const int t = whole ? item : p.dp_tiles + jt;
   const int split = whole ? 0 : (item - p.dp_tiles) - jt * p.splits;
   const int splits = whole ? 1 : p.splits;
-  const int group = t / (kTallGroupRows * col_blocks);
-  const int first_rb = group * kTallGroupRows;
-  const int group_rows = min(row_blocks - first_rb, kTallGroupRows);
-  const int t_in = t - group * kTallGroupRows * col_blocks;
+  const int group = t / (GR * col_blocks);
+  const int first_rb = group * GR;
+  const int group_rows = min(row_blocks - first_rb, GR);
+  const int t_in = t - group * GR * col_blocks;
   const int rb = first_rb + t_in % group_rows, cb = t_in / group_rows;
   const int w0 = cb * kTallWords, m0 = rb * BM;
   const int stages = p.K / BK;
