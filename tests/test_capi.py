@@ -106,8 +106,8 @@ def test_workspace_query_library_gemm_path(lib, monkeypatch):
 def test_product_kernel_query(lib, monkeypatch):
     """grinqh_product_kernel names the kernel each row count and shape takes,
     without a GPU: GEMV to 4 rows, decode to 64, the fused prefill below 256
-    rows, the library GEMM or the large-batch kernel above as the dispatch
-    prefers, the large-batch kernel without a workspace (where its repacked
+    rows (below 129 for weights of at least 192 blocks of 128 columns), the
+    library GEMM or the large-batch kernel above as the dispatch prefers, the large-batch kernel without a workspace (where its repacked
     activations fit the fixed scratch), the fused kernel where neither
     fits."""
     from grinqh import _lib
@@ -116,6 +116,9 @@ def test_product_kernel_query(lib, monkeypatch):
     assert f(1, 4096, 4096)[0] == _lib.KERNEL_GEMV
     assert f(64, 4096, 4096)[0] == _lib.KERNEL_DECODE
     assert f(200, 4096, 4096)[0] == _lib.KERNEL_FUSED
+    assert f(128, 4096, 28672)[0] == _lib.KERNEL_FUSED
+    assert f(129, 4096, 28672)[0] == _lib.KERNEL_TALL           # gate_up: one round of whole tiles
+    assert f(255, 14336, 4096)[0] == _lib.KERNEL_FUSED          # down
     assert f(2048, 4096, 28672)[0] == _lib.KERNEL_LIBRARY
     assert f(512, 4096, 6144)[0] == _lib.KERNEL_LIBRARY
     assert f(512, 4096, 28672) == (_lib.KERNEL_TALL, 512, 1)

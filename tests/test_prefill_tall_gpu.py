@@ -177,6 +177,32 @@ def test_tall_two_waves_per_block(lib, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("mode", ["dense", "union"])
+def test_tall_wide_weight_from_129_rows(lib, dtype, mode, monkeypatch):
+    """Below 256 rows the default dispatch gives the large-batch kernel the
+    weights with at least 192 blocks of 128 columns (Llama-3-8B gate_up, K =
+    4096, N = 28672) from 129 rows, and the fused kernel the rest: at 192 rows
+    one 256-row block per column block, 64 rows of it past the batch, held to
+    the oracle on a slice of the columns (the first 1536 and the last 512;
+    columns are independent), with bias; 128 rows stay on the fused kernel."""
+    from grinqh import _lib
+    monkeypatch.delenv("GRINQH_PREFILL", raising=False)
+    rng = np.random.default_rng(6600)
+    M, K, N, b = 192, 4096, 28672, 8
+    assert _plan(M, K, N, dtype, b, mode)[:2] == (_lib.KERNEL_TALL, 256)
+    assert _plan(128, K, N, dtype, b, mode)[0] == _lib.KERNEL_FUSED
+    W, s, P = _weights(rng, K, N, b, dtype)
+    x = to_dtype_np(rng.standard_normal((M, K)), dtype)
+    bias = to_dtype_np(rng.standard_normal(N), dtype)
+    t = [0.0] + np.quantile(O.union_sigma(x), [0.7, 0.9, 0.98]).tolist() if mode == "union" else [0.0] * 4
+    y = _run(_dev(x, dtype), P, _dev(s, dtype), _dev(bias, dtype), N, b, t, mode)
+    cols = np.r_[0:1536, N - 512:N]
+    pre, fin = _expect(x, W[:, cols], s[:, cols], t, b, mode, dtype, bias[cols])
+    assert_output_close(y[:, torch.from_numpy(cols).cuda()], pre, fin, dtype, bias=bias[cols],
+                        what=f"tall prefill 192 rows {mode} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_tall_ragged_rows_strided(lib, dtype):
     from grinqh import _lib
     """700 rows (the second 512-row block holds 188: one wave partly, three

@@ -117,12 +117,21 @@ int prefill_splits(int64_t M, int64_t K, int64_t N);
 // Large-batch prefill (prefill_tall.hip): (64 * rt) x 128 output tiles over
 // four waves (one per SIMD), x repacked into MFMA fragments and loaded
 // straight into registers, the weight dequantized per 64-row stage into LDS
-// and shared by the block's waves.  From kTallPrefillRows rows, K and the
-// group size multiples of 64, N % 128 == 0 and the repacked x below 2^31
-// bytes.  The first dp_tiles tiles run whole; the others (the last, partly
-// filled round) split K into `splits` ranges, completed in the kernel
-// (partial sums, per-tile counters).
+// and shared by the block's waves.  From kTallPrefillRows rows (from
+// kTallWideRows when the weight has at least kTallWideColBlocks blocks of
+// 128 columns), K and the group size multiples of 64, N % 128 == 0 and the
+// repacked x below 2^31 bytes.  The first dp_tiles tiles run whole; the
+// others (the last, partly filled round) split K into `splits` ranges,
+// completed in the kernel (partial sums, per-tile counters).
 constexpr int64_t kTallPrefillRows = 256;
+// 129-255 rows of a weight this wide fill the GPU with one round of whole
+// 256-row tiles, which takes the same time as at 256 rows, while the fused
+// kernel's grid then needs two row tiles per column block: Llama-3-8B gate_up
+// at 192 / 255 rows took 80.8 / 84.6 us here against 118.2 / 120.9 us fused
+// (graded 98.8 against 139.5 / 143.5).  At 80-128 rows, and for the narrower
+// weights (down, o_proj at 80-255 rows), the fused kernel stays faster.
+constexpr int64_t kTallWideRows = 129;
+constexpr int64_t kTallWideColBlocks = 192;
 struct TallPlan {
   int rt;        // 16-row tiles per wave: 8 (512-row blocks) or 4 (256-row blocks)
   int splits;    // K ranges of the split tiles

@@ -538,7 +538,8 @@ int launch_repack_x(const uint16_t* x, int64_t ldx, int M, int K, uint16_t* xt, 
 
 bool prefill_tall_applies(int64_t M, int64_t K, int64_t N, int64_t ldx, int gs) {
   (void)ldx;  // x is repacked first; the repacked copy is addressed with 32-bit offsets
-  return M >= kTallPrefillRows && K % kTallBK == 0 && gs % kTallBK == 0 && (N / 16) % kTallWords == 0 &&
+  const bool rows_ok = M >= kTallPrefillRows || (M >= kTallWideRows && (N / 16) / kTallWords >= kTallWideColBlocks);
+  return rows_ok && K % kTallBK == 0 && gs % kTallBK == 0 && (N / 16) % kTallWords == 0 &&
          tall_x_bytes(M, K) < ((size_t)1 << 31);
 }
 
