@@ -27,6 +27,7 @@ def _gpu():
     if not torch.cuda.is_available():
         pytest.fail("GPU tests need a HIP device")
     from grinqh import _lib
+    import grinqh.kernel  # noqa: F401  (registers torch.ops.grinqh.gemm_or_gemv, which some tests call)
     _lib.load_library()
 
 
