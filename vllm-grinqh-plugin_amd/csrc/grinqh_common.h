@@ -311,6 +311,14 @@ struct Dequant<F16, SH> {
     const half2_t w = __builtin_bit_cast(half2_t, h) + __builtin_bit_cast(half2_t, negc);  // exact integers
     return __builtin_bit_cast(uint32_t, w * __builtin_bit_cast(half2_t, s2));                // RNE(w * s)
   }
+  // the same with s = half `hi` of sp (two columns' scales): the broadcast
+  // folds into the packed multiply's operand select, so no register holds
+  // the (s, s) pair
+  __device__ __forceinline__ static uint32_t pair_half(uint32_t V0, uint32_t V1, int beta, uint32_t negc, uint32_t sp,
+                                                       int hi) {
+    const _Float16 s = __builtin_bit_cast(half2_t, sp)[hi];
+    return pair(V0, V1, beta, negc, __builtin_bit_cast(uint32_t, half2_t{s, s}));
+  }
 };
 
 template <int SH>

@@ -277,22 +277,17 @@ __global__ __launch_bounds__(256, 1) void prefill_tall_kernel(PrefillParams p) {
     for (int j = 0; j < 4; ++j) prep_code(j);
     prep_scales(sslot);
   };
-  // scale of column tile r: (s, s) for fp16, s * 2^-sh for bf16
-  auto scale_of = [&](int r) -> uint32_t {
-    if constexpr (IS_F16)
-      return perm(s2[r >> 1], s2[r >> 1], (r & 1) ? 0x03020302u : 0x01000100u);
-    else
-      return __float_as_uint(to_f32<DT>((uint16_t)((r & 1) ? (s2[r >> 1] >> 16) : (s2[r >> 1] & 0xFFFFu))) *
-                             (1.0f / (float)(1 << SH)));
-  };
+  // column tile r's scale is half r % 2 of s2[r / 2]: fp16 multiplies by it
+  // broadcast (an operand select of the packed multiply), bf16 by s * 2^-sh
   auto store_w = [&](int buf, int r) {  // column tile r = 4 j + b: k = 2 rp0, 2 rp0 + 1 of the stage
     const int j = r >> 2, b = r & 3;
     uint32_t w;
-    const uint32_t sc = scale_of(r);
     if constexpr (IS_F16) {
-      w = Dequant<F16, SH>::pair(V[j][0], V[j][1], b, negc, sc);
+      w = Dequant<F16, SH>::pair_half(V[j][0], V[j][1], b, negc, s2[r >> 1], r & 1);
     } else {
-      w = bf16_pair(V[j][0], V[j][1], b, cbf[0], cbf[1], __uint_as_float(sc));
+      const float sc = to_f32<DT>((uint16_t)((r & 1) ? (s2[r >> 1] >> 16) : (s2[r >> 1] & 0xFFFFu))) *
+                       (1.0f / (float)(1 << SH));
+      w = bf16_pair(V[j][0], V[j][1], b, cbf[0], cbf[1], sc);
     }
     *reinterpret_cast<uint32_t*>(&s_b[buf][bswz(8 * r + wc, rp0 >> 2) + 2 * (rp0 & 3)]) = w;
   };
