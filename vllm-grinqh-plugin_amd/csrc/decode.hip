@@ -38,6 +38,11 @@
 //     in fp32, as grinqh/kernel.py:148-158 applies scales;
 //   - the scaled weight (17-64 rows in fp16): B = RNE(w_eff * s) in fp16,
 //     accumulated straight into y (no per-group sums, no correction column).
+// The A operand (x) comes from L2 per tile, except at 33-64 rows in fp16:
+// there the two waves that share a K sub-range each load half of the next
+// tile's x straight into LDS (buffer loads to LDS) and read the whole tile
+// from there, after a per-tile handshake through LDS flags, so each x tile is
+// fetched once per K sub-range instead of once per wave.
 //
 // Split-K partials are reduced deterministically: the K sub-ranges of a block
 // through LDS in fixed order; the K ranges of the grid either by the range
@@ -75,10 +80,14 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   constexpr int KW = NWV == 8 ? 4 : 4 / MT;  // K sub-ranges per block
   constexpr int JG = NWV / KW;         // groups of output dwords (waves per K sub-range)
   // tiles of loads in flight ahead of the one unpacked; the scaled path runs
-  // two waves per SIMD on 256 registers, with one tile ahead and its A operand
-  // loaded when the tile starts
+  // two waves per SIMD on 256 registers, with one tile ahead (33-64 rows) and
+  // its A operand through LDS, or two ahead (17-32 rows) and its A operand
+  // loaded from L2 when the tile starts
   constexpr int PF = (SC && MT == 4) ? 1 : 2;
   constexpr bool A_LATE = SC;
+  // 33-64 rows in fp16: the two waves of a K sub-range share its x tiles
+  // through LDS (see s_xr0)
+  constexpr bool XL = A_LATE && PF == 1 && JG == 2;
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
   // A operand is read from global memory (L2-resident) with the plane words,
@@ -108,7 +117,19 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // above 16 rows, graded, no statistic given: this block's rows of the batch
   // statistic, max_m |x[m][k]| as float bits (an entry that is NaN in every
   // row gives 0; every output of such a batch is NaN whatever its grading)
-  __shared__ uint32_t s_sig[AG ? RMAX : 1];
+  // 33-64 rows in fp16: the x tile of each K sub-range (the A operand of its
+  // two waves) comes into LDS by direct buffer-to-LDS loads one tile ahead,
+  // each wave loading half of it, in two slots that are separate LDS arrays
+  // (so that the compiler's wait for one slot's loads does not also wait for
+  // the other's).  s_xflag[w] is the last tile whose half wave w has in LDS.
+  // The statistic above shares the first slot's storage: it is read only
+  // before the first of those loads.
+  constexpr int XR_BYTES = XL ? KW * MT * 1024 : 0;
+  constexpr int SIG_BYTES = AG ? RMAX * 4 : 4;
+  __shared__ __align__(16) unsigned char s_xr0[XR_BYTES > SIG_BYTES ? XR_BYTES : SIG_BYTES];
+  __shared__ __align__(16) unsigned char s_xr1[XR_BYTES > 16 ? XR_BYTES : 16];
+  __shared__ int s_xflag[NWV];
+  uint32_t* s_sig = reinterpret_cast<uint32_t*>(s_xr0);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
   uint32_t* s_off = reinterpret_cast<uint32_t*>(s_pool + X_BYTES);
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(s_pool);
@@ -116,6 +137,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int jg = wave % JG, kw = wave / JG;
+  if (XL && lane == 0) s_xflag[wave] = -(1 << 30);  // read by the partner only after the next barrier
   const int c = lane & 15, q = lane >> 4;
   // logical block = (column block, K range), column blocks fastest, ranges of
   // consecutive logical blocks per XCD (adjacent column blocks share lines)
@@ -387,16 +409,32 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   int gpos = (tile0 + t_begin) % tiles_per_group;
   int gloc = (tile0 + t_begin) / tiles_per_group - g_first;
   uint32_t s2[NJ][4];  // scaled path: (s, s) of the current group's columns
-  auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn) {
+  // this wave's half of x[16*mt + c][rows 8q .. 8q+7 of tile t] (fragments
+  // mt = 2 jg, 2 jg + 1) into slot xr: lane l's 16 bytes land at byte 16 l of
+  // the fragment's KiB; rows m >= M, and tiles past the range, read nothing
+  // (and are never used)
+  auto load_x_lds = [&](int t, unsigned char* xr) {
+    const __amdgpu_buffer_rsrc_t xs = t < t_end ? xsrc : xsrc_none;
+#pragma unroll
+    for (int h = 0; h < MT / 2; ++h) {
+      const int mt = (MT / 2) * jg + h;
+      const int m = 16 * mt + c;
+      const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + t * 32 + 8 * q) * 2) : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xs, (__attribute__((address_space(3))) void*)(xr + (kw * MT + mt) * 1024), 16, (int)off, 0, 0, 0);
+    }
+  };
+  auto step = [&](int t, Tile& Tc, bool prefetch, Tile& Tn, unsigned char* xcur, unsigned char* xnext) {
     const bool first_of_group = (t == t_begin) || (gpos == 0);
     const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
     const int sb = t * 32 + 8 * q;
 
-    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  The scaled path
-    // loads it here from L2, before the next tile's plane words: memory
-    // operations complete in order, so waiting for A then leaves those in
-    // flight (loaded after them, every tile waited for the prefetch's whole
-    // round trip).
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  At 33-64 rows
+    // it is read from the K sub-range's LDS slot, filled half by each of its
+    // two waves one tile ahead; at 17-32 rows the scaled path loads it here
+    // from L2, before the next tile's plane words: memory operations complete
+    // in order, so waiting for A then leaves those in flight (loaded after
+    // them, every tile waited for the prefetch's whole round trip).
     u32x4_t A[MT];
     auto load_a = [&]() {
 #pragma unroll
@@ -412,7 +450,29 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
         }
       }
     };
-    if constexpr (A_LATE) {
+    if constexpr (XL) {
+      // own half of tile t (its loads waited for by the compiler), then the
+      // handshake: publish it, and wait until the partner has published its
+      // half, which also means it has read tile t - 1's slot, the one the
+      // next loads overwrite.  Both waves publish before they wait, so every
+      // wait ends.
+      const unsigned char* xb = xcur + kw * MT * 1024 + lane * 16;
+      // one dword of the own half read back: the compiler waits for this
+      // wave's loads into the slot before it
+      const uint32_t probe = *reinterpret_cast<const uint32_t*>(xb + (MT / 2) * jg * 1024);
+      asm volatile("" ::"v"(probe));
+      if (lane == 0) __hip_atomic_store(&s_xflag[wave], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      // (bounded: a wait that outlasted ~2^20 sleeps would end, with a wrong
+      // tile, rather than hang; the partner publishes within microseconds)
+      for (int spin = 0; spin < (1 << 20) &&
+                         __builtin_amdgcn_readfirstlane(__hip_atomic_load(&s_xflag[wave ^ 1], __ATOMIC_RELAXED,
+                                                                          __HIP_MEMORY_SCOPE_WORKGROUP)) < t;
+           ++spin)
+        __builtin_amdgcn_s_sleep(1);
+      if (prefetch) load_x_lds(t + 1, xnext);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(xb + mt * 1024);
+    } else if constexpr (A_LATE) {
       load_a();
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -512,22 +572,24 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       issue(t_begin + 1, TB);
       stage_scales();
       for (; t + 3 <= t_end; t += 3) {
-        step(t, TA, true, TC);
-        step(t + 1, TB, true, TA);
-        step(t + 2, TC, true, TB);
+        step(t, TA, true, TC, s_xr0, s_xr1);
+        step(t + 1, TB, true, TA, s_xr0, s_xr1);
+        step(t + 2, TC, true, TB, s_xr0, s_xr1);
       }
       // at most two tiles left, already loaded into TA and TB
-      if (t < t_end) step(t, TA, false, TC);
-      if (t + 1 < t_end) step(t + 1, TB, false, TC);
+      if (t < t_end) step(t, TA, false, TC, s_xr0, s_xr1);
+      if (t + 1 < t_end) step(t + 1, TB, false, TC, s_xr0, s_xr1);
     } else {
       // two tile buffers: tile t+1 is in flight while tile t is unpacked
+      // the first x tile before the first plane words, as in every step
+      if constexpr (XL) load_x_lds(t_begin, s_xr0);
       issue(t_begin, TA);
       stage_scales();
       for (; t + 2 <= t_end; t += 2) {
-        step(t, TA, true, TB);
-        step(t + 1, TB, true, TA);
+        step(t, TA, true, TB, s_xr0, s_xr1);
+        step(t + 1, TB, true, TA, s_xr1, s_xr0);
       }
-      if (t < t_end) step(t, TA, false, TB);
+      if (t < t_end) step(t, TA, false, TB, s_xr0, s_xr1);
     }
   }
 
