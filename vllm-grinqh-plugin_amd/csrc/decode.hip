@@ -38,11 +38,12 @@
 //     in fp32, as grinqh/kernel.py:148-158 applies scales;
 //   - the scaled weight (17-64 rows in fp16): B = RNE(w_eff * s) in fp16,
 //     accumulated straight into y (no per-group sums, no correction column).
-// The A operand (x) comes from L2 per tile, except at 33-64 rows in fp16:
-// there the two waves that share a K sub-range each load half of the next
-// tile's x straight into LDS (buffer loads to LDS) and read the whole tile
-// from there, after a per-tile handshake through LDS flags, so each x tile is
-// fetched once per K sub-range instead of once per wave.
+// Above 16 rows the A operand (x) is not staged for the whole K range: in
+// fp16 (17-64 rows) the two waves that share a K sub-range each load half of
+// the next tile's x straight into LDS (buffer loads to LDS) and read the
+// whole tile from there, after a per-tile handshake through LDS flags, so
+// each x tile is fetched once per K sub-range instead of once per wave; bf16
+// loads it from L2 with the tile's plane words.
 //
 // Split-K partials are reduced deterministically: the K sub-ranges of a block
 // through LDS in fixed order; the K ranges of the grid either by the range
@@ -80,18 +81,18 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   constexpr int KW = NWV == 8 ? 4 : 4 / MT;  // K sub-ranges per block
   constexpr int JG = NWV / KW;         // groups of output dwords (waves per K sub-range)
   // tiles of loads in flight ahead of the one unpacked; the scaled path runs
-  // two waves per SIMD on 256 registers, with one tile ahead (33-64 rows) and
-  // its A operand through LDS, or two ahead (17-32 rows) and its A operand
-  // loaded from L2 when the tile starts
+  // two waves per SIMD on 256 registers, with one tile ahead (33-64 rows) or
+  // two (17-32 rows), and its A operand through LDS
   constexpr int PF = (SC && MT == 4) ? 1 : 2;
-  constexpr bool A_LATE = SC;
-  // 33-64 rows in fp16: the two waves of a K sub-range share its x tiles
+  // 17-64 rows in fp16: the two waves of a K sub-range share its x tiles
   // through LDS (see s_xr0)
-  constexpr bool XL = A_LATE && PF == 1 && JG == 2;
+  constexpr bool XL = SC;
+  static_assert(!XL || JG == 2, "x tiles are shared by the two waves of a K sub-range");
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
-  // A operand is read from global memory (L2-resident) with the plane words,
-  // and grading uses the batch statistic of the block's rows, reduced from x
+  // A operand comes tile by tile from global memory (L2-resident; through the
+  // shared LDS slots in fp16, with the plane words in bf16), and grading
+  // uses the batch statistic of the block's rows, reduced from x
   // in the prologue (or given by the caller), so the K range is not limited
   // by staging x.
   constexpr bool AG = MT >= 2;
@@ -117,17 +118,19 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // above 16 rows, graded, no statistic given: this block's rows of the batch
   // statistic, max_m |x[m][k]| as float bits (an entry that is NaN in every
   // row gives 0; every output of such a batch is NaN whatever its grading)
-  // 33-64 rows in fp16: the x tile of each K sub-range (the A operand of its
+  // 17-64 rows in fp16: the x tile of each K sub-range (the A operand of its
   // two waves) comes into LDS by direct buffer-to-LDS loads one tile ahead,
-  // each wave loading half of it, in two slots that are separate LDS arrays
-  // (so that the compiler's wait for one slot's loads does not also wait for
-  // the other's).  s_xflag[w] is the last tile whose half wave w has in LDS.
-  // The statistic above shares the first slot's storage: it is read only
-  // before the first of those loads.
+  // each wave loading half of it, in PF + 1 slots (one per tile buffer of
+  // the unrolled loop) that are separate LDS arrays (so that the compiler's
+  // wait for one slot's loads does not also wait for the others').
+  // s_xflag[w] is the last tile whose half wave w has in LDS.  The statistic
+  // above shares the first slot's storage: it is read only before the first
+  // of those loads.
   constexpr int XR_BYTES = XL ? KW * MT * 1024 : 0;
   constexpr int SIG_BYTES = AG ? RMAX * 4 : 4;
   __shared__ __align__(16) unsigned char s_xr0[XR_BYTES > SIG_BYTES ? XR_BYTES : SIG_BYTES];
   __shared__ __align__(16) unsigned char s_xr1[XR_BYTES > 16 ? XR_BYTES : 16];
+  __shared__ __align__(16) unsigned char s_xr2[(XL && PF == 2 && XR_BYTES > 16) ? XR_BYTES : 16];
   __shared__ int s_xflag[NWV];
   uint32_t* s_sig = reinterpret_cast<uint32_t*>(s_xr0);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(s_pool);
@@ -368,7 +371,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // plane words of one tile (and, above 16 rows, its A operand)
   struct Tile {
     uint32_t D[8][Z];
-    u32x4_t A[AG && !A_LATE ? MT : 1];
+    u32x4_t A[AG && !XL ? MT : 1];
   };
   const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(p.x), (short)0, (int)((uint64_t)p.M * p.ldx * 2u), 0x00020000);
@@ -392,7 +395,7 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
         T.D[e][z] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, (int)(oz + lane_off), 0, 0);
       }
     }
-    if constexpr (AG && !A_LATE) {  // x[16*mt + c][rows 8q .. 8q+7 of the tile]; rows m >= M read 0
+    if constexpr (AG && !XL) {  // x[16*mt + c][rows 8q .. 8q+7 of the tile]; rows m >= M read 0
       const __amdgpu_buffer_rsrc_t xs = live ? xsrc : xsrc_none;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -429,21 +432,16 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
     const int sb = t * 32 + 8 * q;
 
-    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  At 33-64 rows
-    // it is read from the K sub-range's LDS slot, filled half by each of its
-    // two waves one tile ahead; at 17-32 rows the scaled path loads it here
-    // from L2, before the next tile's plane words: memory operations complete
-    // in order, so waiting for A then leaves those in flight (loaded after
-    // them, every tile waited for the prefetch's whole round trip).
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  At 17-64 rows in
+    // fp16 it is read from the K sub-range's LDS slot, filled half by each of
+    // its two waves one tile ahead (loaded before the next tile's plane
+    // words: memory operations complete in order, so waiting for it leaves
+    // those in flight).
     u32x4_t A[MT];
     auto load_a = [&]() {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        if constexpr (A_LATE) {  // rows m >= M read 0
-          const int m = 16 * mt + c;
-          const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + sb) * 2) : 0x80000000u;
-          A[mt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xsrc, (int)off, 0, 0));
-        } else if constexpr (AG) {
+        if constexpr (AG) {
           A[mt] = Tc.A[mt];
         } else {
           A[mt] = *reinterpret_cast<const u32x4_t*>(&s_x[(16 * mt + c) * XS + sb]);
@@ -469,16 +467,15 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
                                                                           __HIP_MEMORY_SCOPE_WORKGROUP)) < t;
            ++spin)
         __builtin_amdgcn_s_sleep(1);
-      if (prefetch) load_x_lds(t + 1, xnext);
+      // (always: a tile past the range reads nothing; at 17-32 rows the last
+      // two steps take no plane prefetch but the second still needs its x)
+      load_x_lds(t + 1, xnext);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) A[mt] = *reinterpret_cast<const u32x4_t*>(xb + mt * 1024);
-    } else if constexpr (A_LATE) {
-      load_a();
-      __builtin_amdgcn_sched_barrier(0);
     }
     if (prefetch) issue(t + PF, Tn);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!A_LATE) load_a();
+    if constexpr (!XL) load_a();
 
     const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(&s_bv[sb]);
 
@@ -567,18 +564,21 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     Tile TA, TB, TC;
     int t = t_begin;
     if constexpr (PF == 2) {
-      // three tile buffers: tiles t+1 and t+2 are in flight while tile t is unpacked
+      // three tile buffers: tiles t+1 and t+2 are in flight while tile t is
+      // unpacked; the first x tile before the first plane words, as in every
+      // step
+      if constexpr (XL) load_x_lds(t_begin, s_xr0);
       issue(t_begin, TA);
       issue(t_begin + 1, TB);
       stage_scales();
       for (; t + 3 <= t_end; t += 3) {
         step(t, TA, true, TC, s_xr0, s_xr1);
-        step(t + 1, TB, true, TA, s_xr0, s_xr1);
-        step(t + 2, TC, true, TB, s_xr0, s_xr1);
+        step(t + 1, TB, true, TA, s_xr1, s_xr2);
+        step(t + 2, TC, true, TB, s_xr2, s_xr0);
       }
       // at most two tiles left, already loaded into TA and TB
       if (t < t_end) step(t, TA, false, TC, s_xr0, s_xr1);
-      if (t + 1 < t_end) step(t + 1, TB, false, TC, s_xr0, s_xr1);
+      if (t + 1 < t_end) step(t + 1, TB, false, TC, s_xr1, s_xr2);
     } else {
       // two tile buffers: tile t+1 is in flight while tile t is unpacked
       // the first x tile before the first plane words, as in every step
