@@ -39,11 +39,11 @@
 //   - the scaled weight (17-64 rows in fp16): B = RNE(w_eff * s) in fp16,
 //     accumulated straight into y (no per-group sums, no correction column).
 // Above 16 rows the A operand (x) is not staged for the whole K range: in
-// fp16 (17-64 rows) the two waves that share a K sub-range each load half of
-// the next tile's x straight into LDS (buffer loads to LDS) and read the
-// whole tile from there, after a per-tile handshake through LDS flags, so
-// each x tile is fetched once per K sub-range instead of once per wave; bf16
-// loads it from L2 with the tile's plane words.
+// fp16 the two waves that share a K sub-range each load half of the next
+// tile's x straight into LDS (buffer loads to LDS) and read the whole tile
+// from there, after a per-tile handshake through LDS flags, so each x tile is
+// fetched once per K sub-range instead of once per wave; bf16 loads it from
+// L2 with the tile's plane words.
 //
 // Split-K partials are reduced deterministically: the K sub-ranges of a block
 // through LDS in fixed order; the K ranges of the grid either by the range
@@ -84,10 +84,14 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // two waves per SIMD on 256 registers, with one tile ahead (33-64 rows) or
   // two (17-32 rows), and its A operand through LDS
   constexpr int PF = (SC && MT == 4) ? 1 : 2;
-  // 17-64 rows in fp16: the two waves of a K sub-range share its x tiles
-  // through LDS (see s_xr0)
+  // 17-64 rows in fp16: the JG waves of a K sub-range share its x tiles
+  // through LDS (see s_xr0), each loading XF of a tile's MT fragments.  bf16
+  // (one wave per SIMD, none to cover a wave's wait at the handshake) loads
+  // them with the plane words two tiles ahead: shared, its 48-64-row
+  // products took 17-25 % longer.
   constexpr bool XL = SC;
-  static_assert(!XL || JG == 2, "x tiles are shared by the two waves of a K sub-range");
+  constexpr int XF = MT / JG;
+  static_assert(!XL || (XF >= 1 && XF * JG == MT), "each wave of a K sub-range loads whole fragments");
   constexpr int SH = 8 - 2 * Z;
   // Up to 16 rows x is staged in LDS for the block's K range; above that the
   // A operand comes tile by tile from global memory (L2-resident; through the
@@ -119,8 +123,8 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   // statistic, max_m |x[m][k]| as float bits (an entry that is NaN in every
   // row gives 0; every output of such a batch is NaN whatever its grading)
   // 17-64 rows in fp16: the x tile of each K sub-range (the A operand of its
-  // two waves) comes into LDS by direct buffer-to-LDS loads one tile ahead,
-  // each wave loading half of it, in PF + 1 slots (one per tile buffer of
+  // JG waves) comes into LDS by direct buffer-to-LDS loads one tile ahead,
+  // each wave loading XF of its fragments, in PF + 1 slots (one per tile buffer of
   // the unrolled loop) that are separate LDS arrays (so that the compiler's
   // wait for one slot's loads does not also wait for the others').
   // s_xflag[w] is the last tile whose half wave w has in LDS.  The statistic
@@ -412,15 +416,15 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
   int gpos = (tile0 + t_begin) % tiles_per_group;
   int gloc = (tile0 + t_begin) / tiles_per_group - g_first;
   uint32_t s2[NJ][4];  // scaled path: (s, s) of the current group's columns
-  // this wave's half of x[16*mt + c][rows 8q .. 8q+7 of tile t] (fragments
-  // mt = 2 jg, 2 jg + 1) into slot xr: lane l's 16 bytes land at byte 16 l of
-  // the fragment's KiB; rows m >= M, and tiles past the range, read nothing
-  // (and are never used)
+  // this wave's share of x[16*mt + c][rows 8q .. 8q+7 of tile t] (fragments
+  // mt = XF jg .. XF jg + XF - 1) into slot xr: lane l's 16 bytes land at
+  // byte 16 l of the fragment's KiB; rows m >= M, and tiles past the range,
+  // read nothing (and are never used)
   auto load_x_lds = [&](int t, unsigned char* xr) {
     const __amdgpu_buffer_rsrc_t xs = t < t_end ? xsrc : xsrc_none;
 #pragma unroll
-    for (int h = 0; h < MT / 2; ++h) {
-      const int mt = (MT / 2) * jg + h;
+    for (int h = 0; h < XF; ++h) {
+      const int mt = XF * jg + h;
       const int m = 16 * mt + c;
       const uint32_t off = m < p.M ? (uint32_t)(((int64_t)m * p.ldx + row0 + t * 32 + 8 * q) * 2) : 0x80000000u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -432,11 +436,11 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
     const bool last_of_group = (t + 1 == t_end) || (gpos + 1 == tiles_per_group);
     const int sb = t * 32 + 8 * q;
 
-    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  At 17-64 rows in
-    // fp16 it is read from the K sub-range's LDS slot, filled half by each of
-    // its two waves one tile ahead (loaded before the next tile's plane
-    // words: memory operations complete in order, so waiting for it leaves
-    // those in flight).
+    // A operand: x[16*mt + c][rows 8q .. 8q+7 of the tile].  At 17-64 rows
+    // it is read from the K sub-range's LDS slot, filled in shares by its
+    // waves one tile ahead (loaded before the next tile's plane words: memory
+    // operations complete in order, so waiting for it leaves those in
+    // flight).
     u32x4_t A[MT];
     auto load_a = [&]() {
 #pragma unroll
@@ -449,24 +453,28 @@ __global__ __launch_bounds__((64 * decode_waves<DT, MT>()), 1) void decode_kerne
       }
     };
     if constexpr (XL) {
-      // own half of tile t (its loads waited for by the compiler), then the
-      // handshake: publish it, and wait until the partner has published its
-      // half, which also means it has read tile t - 1's slot, the one the
-      // next loads overwrite.  Both waves publish before they wait, so every
-      // wait ends.
+      // own share of tile t (its loads waited for by the compiler), then the
+      // handshake: publish it, and wait until every other wave of the K
+      // sub-range has published its share, which also means it has read the
+      // slots of earlier tiles, the one the next loads overwrite among them.
+      // Every wave publishes before it waits, so every wait ends.
       const unsigned char* xb = xcur + kw * MT * 1024 + lane * 16;
-      // one dword of the own half read back: the compiler waits for this
+      // one dword of the own share read back: the compiler waits for this
       // wave's loads into the slot before it
-      const uint32_t probe = *reinterpret_cast<const uint32_t*>(xb + (MT / 2) * jg * 1024);
+      const uint32_t probe = *reinterpret_cast<const uint32_t*>(xb + XF * jg * 1024);
       asm volatile("" ::"v"(probe));
       if (lane == 0) __hip_atomic_store(&s_xflag[wave], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       // (bounded: a wait that outlasted ~2^20 sleeps would end, with a wrong
-      // tile, rather than hang; the partner publishes within microseconds)
-      for (int spin = 0; spin < (1 << 20) &&
-                         __builtin_amdgcn_readfirstlane(__hip_atomic_load(&s_xflag[wave ^ 1], __ATOMIC_RELAXED,
-                                                                          __HIP_MEMORY_SCOPE_WORKGROUP)) < t;
-           ++spin)
-        __builtin_amdgcn_s_sleep(1);
+      // tile, rather than hang; the others publish within microseconds)
+#pragma unroll
+      for (int pj = 0; pj < JG; ++pj) {
+        if (pj == jg) continue;
+        for (int spin = 0; spin < (1 << 20) &&
+                           __builtin_amdgcn_readfirstlane(__hip_atomic_load(
+                               &s_xflag[kw * JG + pj], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < t;
+             ++spin)
+          __builtin_amdgcn_s_sleep(1);
+      }
       // (always: a tile past the range reads nothing; at 17-32 rows the last
       // two steps take no plane prefetch but the second still needs its x)
       load_x_lds(t + 1, xnext);
