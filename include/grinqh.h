@@ -171,8 +171,8 @@ int grinqh_gemv_batch_union_sigma(const void* x, int64_t M, int64_t K, int64_t l
  * of its own (no hipMalloc, hipFree or allocating library routine).  A few
  * kernel instantiations spill registers to the private-segment (scratch)
  * memory that the HIP runtime sets up for a device's queues (the large-batch
- * kernel's 512-row blocks, the 33-64-row decode kernel: tests check the
- * build's resource report); a caller that must see no runtime allocation at
+ * kernel's 512-row blocks: tests check the build's resource report); a
+ * caller that must see no runtime allocation at
  * all runs one call of each shape class first.  The library-GEMM prefill path
  * (a 2*N*K dense weight buffer) is not taken: from 256 rows the hand-written
  * large-batch kernel runs where its repacked activations fit the array, else
