@@ -20,7 +20,9 @@ pytestmark = pytest.mark.gpu
 
 REPEATS = 8
 SHAPES = [(4096, 6144), (4096, 28672), (14336, 4096)]
-ROWS = [1, 3, 16, 40, 64, 128]
+# 20 and 33: the 17-32- and 33-64-row decode kernels with rows past the batch,
+# whose two waves per K sub-range share each x tile through LDS
+ROWS = [1, 3, 16, 20, 33, 40, 64, 128]
 
 
 @pytest.fixture(scope="module")
