@@ -783,12 +783,15 @@ def test_errors_are_raised_not_computed():
         torch.ops.grinqh.gemm_or_gemv(x48, P[:48], _tdt(s, "float16"), None, 8, 128, 64, [0.0] * 4)
 
 
-def test_graph_capture_replay_matches_eager():
+@pytest.mark.parametrize("M", [4, 20, 64])
+def test_graph_capture_replay_matches_eager(M):
     """The op enqueues only kernels (no memset, no host sync): capture it in a
-    HIP graph and replay it several times with eager work in between."""
+    HIP graph and replay it several times with eager work in between (GEMV,
+    and the 17-32- and 33-64-row decode kernels, whose waves share x tiles
+    through LDS)."""
     from grinqh.kernel import grinqh_gemv_batch_union
-    rng = np.random.default_rng(8)
-    W, x, s = _setup(rng, 4096, 4096, 8, "float16", M=4, scale_sd=0.01)
+    rng = np.random.default_rng(8 + M)
+    W, x, s = _setup(rng, 4096, 4096, 8, "float16", M=M, scale_sd=0.01)
     P, st = _prepare(W, 8), _tdt(s, "float16")
     xin = _tdt(x, "float16")
     t = [0.0, 0.5, 1.0, 2.0]
